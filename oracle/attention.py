@@ -1,0 +1,181 @@
+"""CPU oracle for block-sparse causal GQA prefill attention.
+
+TEST INFRASTRUCTURE ONLY.  Nothing in the shipped package imports this file;
+only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it,
+as the checker of the HIP kernels.
+
+Restates the reference's PyTorch oracle, sparse/attention.py:276-364, in
+numpy float32:
+  for each query block qb, batch b and KV head g (sparse/attention.py:276-281)
+    ids  = selected[b, g, qb][selected >= 0]            (:282-289; empty -> ValueError)
+    keys = ids * block + arange(block), keeping keys < T (:294-297)
+    s    = (q_blk @ k_sel^T) / sqrt(D) in float32       (:303-309)
+    s[key > query] = finfo.min                          (:313-314)
+    out  = softmax(s) @ v_sel                           (:356-359)
+and returns [B, T, Hq, D] (:364).
+
+Deliberate, documented choices where the reference has no single answer:
+  * block IDs above the query block are dropped.  In the reference oracle such
+    a block is fully masked and adds exactly zero weight whenever the row has
+    any causal key; for a row made only of future blocks the reference's
+    backends disagree (its oracle averages V uniformly, its Triton kernel
+    yields NaN).  Here such a row counts as empty;
+  * duplicated IDs are kept and attended twice, as the reference oracle does;
+  * ``scale`` defaults to 1/sqrt(D) (the reference divides by math.sqrt(D));
+  * ``qblocks_subset`` computes only the listed query blocks (the others stay
+    zero), so full-size configurations can be spot-checked row by row.
+
+Pinned by tests/test_oracle_attention.py against the reference's own known
+answers (tests/test_sparse_attention.py:32-87 there), an independent dense
+closed form, a pure-Python brute force and structural invariants.
+"""
+import math
+
+import numpy as np
+
+F32_MIN = np.finfo(np.float32).min
+
+
+def _softmax_rows(s):
+    s = s - s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    return p / p.sum(axis=-1, keepdims=True)
+
+
+def _attend_group(qblk, keys, vals, q_pos, key_idx, scale):
+    """qblk [H, n, D], keys/vals [m, D] -> [H, n, D] (float32)."""
+    s = np.matmul(qblk, keys.T) * np.float32(scale) if scale is not None else \
+        np.matmul(qblk, keys.T) / np.float32(math.sqrt(qblk.shape[-1]))
+    causal = key_idx[None, :] <= q_pos[:, None]
+    s = np.where(causal[None], s, F32_MIN)
+    return np.matmul(_softmax_rows(s), vals).astype(np.float32)
+
+
+def _sparse_attention(q, k, v, blocks_for, block_size, scale, empty, qblocks_subset=None):
+    q = np.asarray(q, dtype=np.float32)
+    k = np.asarray(k, dtype=np.float32)
+    v = np.asarray(v, dtype=np.float32)
+    B, Hq, T, D = q.shape
+    Hkv = k.shape[1]
+    if Hq % Hkv:
+        raise ValueError("query heads must be divisible by KV heads")
+    G = Hq // Hkv
+    qblocks = (T + block_size - 1) // block_size
+    out = np.zeros((B, Hq, T, D), dtype=np.float32)
+    offs = np.arange(block_size)
+    for qb in (range(qblocks) if qblocks_subset is None else qblocks_subset):
+        q0, q1 = qb * block_size, min((qb + 1) * block_size, T)
+        q_pos = np.arange(q0, q1)
+        for b in range(B):
+            for g in range(Hkv):
+                per_head = blocks_for(b, g, qb)
+                if isinstance(per_head, list):  # one list per query head
+                    work = [(slice(g * G + h, g * G + h + 1), per_head[h]) for h in range(G)]
+                else:  # one list shared by the KV head's G query heads
+                    work = [(slice(g * G, (g + 1) * G), per_head)]
+                for heads, ids in work:
+                    ids = np.asarray(ids, dtype=np.int64)
+                    ids = ids[(ids >= 0) & (ids <= qb)]
+                    if ids.size == 0:
+                        if empty == "zero":
+                            continue
+                        raise ValueError(
+                            "selected_blocks leaves an attention row empty at "
+                            f"batch={b}, kv_head={g}, query_block={qb}")
+                    key_idx = (ids[:, None] * block_size + offs[None, :]).reshape(-1)
+                    key_idx = key_idx[key_idx < T]
+                    out[b, heads, q0:q1] = _attend_group(
+                        q[b, heads, q0:q1], k[b, g, key_idx], v[b, g, key_idx],
+                        q_pos, key_idx, scale)
+    return out.transpose(0, 2, 1, 3).copy()
+
+
+def sparse_attention_index(q, k, v, idx, block_size=64, scale=None, empty="raise",
+                           qblocks_subset=None):
+    """Padded direct-index lists ``idx [B, Hkv, Qb, K]`` -> ``[B, T, Hq, D]``."""
+    idx = np.asarray(idx)
+    return _sparse_attention(q, k, v, lambda b, g, qb: idx[b, g, qb], block_size, scale, empty,
+                             qblocks_subset)
+
+
+def sparse_attention_csr(q, k, v, indptr, indices, block_size=64, scale=None, empty="raise",
+                         qblocks_subset=None):
+    """CSR lists, row ``(b*Hkv + g)*Qb + qb`` -> ``[B, T, Hq, D]``."""
+    indptr = np.asarray(indptr)
+    indices = np.asarray(indices)
+    T = np.asarray(q).shape[2]
+    Hkv = np.asarray(k).shape[1]
+    qblocks = (T + block_size - 1) // block_size
+
+    def blocks_for(b, g, qb):
+        r = (b * Hkv + g) * qblocks + qb
+        return indices[indptr[r]:indptr[r + 1]]
+
+    return _sparse_attention(q, k, v, blocks_for, block_size, scale, empty, qblocks_subset)
+
+
+def sparse_attention_mask(q, k, v, mask, block_size=64, scale=None, empty="raise",
+                          qblocks_subset=None):
+    """Boolean block mask ``[B, Hm, Qb, >=Qb]`` with Hm == Hq or Hkv."""
+    mask = np.asarray(mask).astype(bool)
+    Hq = np.asarray(q).shape[1]
+    Hkv = np.asarray(k).shape[1]
+    G = Hq // Hkv
+    Hm = mask.shape[1]
+
+    def blocks_for(b, g, qb):
+        if Hm == Hq and G > 1:
+            rows = [np.nonzero(mask[b, g * G + h, qb, :qb + 1])[0] for h in range(G)]
+            if all(np.array_equal(rows[0], r) for r in rows[1:]):
+                return rows[0]
+            return rows
+        return np.nonzero(mask[b, g, qb, :qb + 1])[0]
+
+    return _sparse_attention(q, k, v, blocks_for, block_size, scale, empty, qblocks_subset)
+
+
+def dense_causal_attention(q, k, v, scale=None):
+    """Closed form: full [T, T] causal softmax attention, GQA by head repetition.
+
+    Independent of the block gather above; used to pin it (all causal blocks
+    selected must reproduce this)."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    B, Hq, T, D = q.shape
+    G = Hq // k.shape[1]
+    kr = np.repeat(k, G, axis=1)
+    vr = np.repeat(v, G, axis=1)
+    s = np.matmul(q, kr.transpose(0, 1, 3, 2)) * (scale if scale is not None else 1.0 / math.sqrt(D))
+    future = np.triu(np.ones((T, T), dtype=bool), k=1)
+    s = np.where(future[None, None], -np.inf, s)
+    s = s - s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=-1, keepdims=True)
+    return np.matmul(p, vr).transpose(0, 2, 1, 3)
+
+
+def attention_bruteforce(q, k, v, key_sets, scale=None):
+    """Pure-Python loops (math.exp, no numpy reductions) for tiny inputs.
+
+    key_sets(b, hq, t) -> iterable of key token indices attended by query t of
+    query head hq.  Returns nested lists [B][T][Hq][D]."""
+    q = np.asarray(q, dtype=np.float64).tolist()
+    k = np.asarray(k, dtype=np.float64).tolist()
+    v = np.asarray(v, dtype=np.float64).tolist()
+    B, Hq, T, D = len(q), len(q[0]), len(q[0][0]), len(q[0][0][0])
+    G = Hq // len(k[0])
+    sc = scale if scale is not None else 1.0 / math.sqrt(D)
+    out = [[[[0.0] * D for _ in range(Hq)] for _ in range(T)] for _ in range(B)]
+    for b in range(B):
+        for h in range(Hq):
+            g = h // G
+            for t in range(T):
+                keys = list(key_sets(b, h, t))
+                scores = [sum(q[b][h][t][d] * k[b][g][j][d] for d in range(D)) * sc for j in keys]
+                mx = max(scores)
+                w = [math.exp(s - mx) for s in scores]
+                z = sum(w)
+                for d in range(D):
+                    out[b][t][h][d] = sum(wi * v[b][g][j][d] for wi, j in zip(w, keys)) / z
+    return out

@@ -1,0 +1,506 @@
+// Block-sparse causal GQA prefill forward for gfx950.
+//
+// Semantics follow the reference PyTorch path sparse/attention.py:276-364 and
+// the kernels it stands in for (kernels/seerattention_direct_index_triton.py:
+// 27-121, kernels/seerattention_triton.py:18-68): for every query token t of
+// query block qb and query head h, softmax(q_t . k_j * scale) over the keys j
+// of the selected 64-token key blocks of KV head h / G with j <= t, applied to
+// v_j.  Scores and the softmax run in fp32; P is rounded to the MFMA input
+// type before P.V, as the reference kernels do (p.to(v.dtype)).
+//
+// Work decomposition (MI355X-first, not the reference's one-head-per-program):
+//   * one workgroup per (batch, KV head, query block, part); the 2G tiles of
+//     32 query rows (G query heads x 2 halves of the 64-row block) of that
+//     KV head are spread over the parts, one tile per wave;
+//   * every selected K/V block is loaded from HBM/L2 once per workgroup into
+//     LDS and shared by all of its waves (GQA packing: 7x less K/V traffic than
+//     one head per program at Qwen2-7B's 28/4 heads);
+//   * S^T = K Q^T on 32x32x16 MFMA puts one query per lane column, so the
+//     row max / row sum of the online softmax are per-lane register reductions
+//     plus one exchange with lane ^ 32;
+//   * O^T = V^T P^T takes P straight from the S^T accumulators as the B
+//     operand; V is transposed while it is staged into LDS, with its 64 keys
+//     stored in the order the accumulator layout hands them out (key bits 2
+//     and 3 swapped), so every MFMA operand is one 16-byte LDS read;
+//   * K/V staging is double-buffered: the next block's global loads are in
+//     flight while the current block is on the matrix cores; one barrier per
+//     block;
+//   * skipped blocks are never touched: the block list is walked once and only
+//     listed blocks are loaded.
+#pragma once
+
+#include <type_traits>
+
+#include "common.h"
+
+namespace spruce {
+
+constexpr int kBlock = 64;
+
+enum : int { kModePadded = 0, kModeCsr = 1, kModeMask = 2 };
+
+struct AttnParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  int64_t qs[4], ks[4], vs[4], os[4];
+  int B, Hq, Hkv, T, G, Qb, parts;
+  float cs;    // multiplier of raw scores inside exp2 (scale*log2 e, or 1 when Q is prescaled)
+  float qmul;  // multiplier applied to Q before rounding when prescaled
+  int prescale;
+  // padded index list
+  const int32_t* idx;
+  int64_t is[4];
+  int K;
+  // CSR list
+  const int32_t* indptr;
+  const int32_t* indices;
+  int nnz;
+  const int32_t* row_order;
+  // block mask
+  const uint8_t* mask;
+  int64_t ms[4];
+  int mask_per_qhead;
+};
+
+struct F32x8 {
+  float4 a, b;
+};
+template <typename TIn>
+using raw8_t = typename std::conditional<TIn::bytes == 2, uint4, F32x8>::type;
+
+template <typename TIn>
+__device__ __forceinline__ raw8_t<TIn> raw_load8(const char* p, bool valid) {
+  raw8_t<TIn> r{};
+  if (valid) r = *reinterpret_cast<const raw8_t<TIn>*>(p);
+  return r;
+}
+
+template <typename TIn, bool F16>
+__device__ __forceinline__ uint4 raw_to_mfma(const raw8_t<TIn>& r) {
+  if constexpr (TIn::bytes == 2) {
+    return r;
+  } else {
+    return uint4{pack2<F16>(r.a.x, r.a.y), pack2<F16>(r.a.z, r.a.w),
+                 pack2<F16>(r.b.x, r.b.y), pack2<F16>(r.b.z, r.b.w)};
+  }
+}
+
+__device__ __forceinline__ uint32_t elem16(const uint4& r, int e) {
+  const uint32_t w = (e >> 1) == 0 ? r.x : (e >> 1) == 1 ? r.y : (e >> 1) == 2 ? r.z : r.w;
+  return (e & 1) ? (w >> 16) : (w & 0xffffu);
+}
+
+// Position of key `key` (0..63) inside a V^T row: bits 2 and 3 swapped, which
+// is the order in which the S^T accumulator registers present the keys.
+__device__ __forceinline__ int vt_pos(int key) {
+  return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
+}
+
+// ------------------------------------------------------------ block lists
+// Each iterator yields the usable key blocks of one (batch, KV head, query
+// block) row in list order: ids in [0, qb].  `en` says whether the wave's own
+// query head attends the block (only the per-query-head mask can say no).
+// All lanes of all waves walk the same sequence.
+template <int MODE>
+struct BlockIter;
+
+template <>
+struct BlockIter<kModePadded> {
+  const int32_t* row;
+  int64_t stride;
+  int n, pos, qb;
+  __device__ void init(const AttnParams& p, int b, int g, int qb_, int, int, int) {
+    row = p.idx + (int64_t)b * p.is[0] + (int64_t)g * p.is[1] + (int64_t)qb_ * p.is[2];
+    stride = p.is[3];
+    n = p.K;
+    pos = 0;
+    qb = qb_;
+  }
+  __device__ bool next(int& id, bool& en) {
+    while (pos < n) {
+      const int v = __builtin_amdgcn_readfirstlane(row[(int64_t)pos * stride]);
+      ++pos;
+      if (v >= 0 && v <= qb) {
+        id = v;
+        en = true;
+        return true;
+      }
+    }
+    return false;
+  }
+};
+
+template <>
+struct BlockIter<kModeCsr> {
+  const int32_t* row;
+  int n, pos, qb;
+  __device__ void init(const AttnParams& p, int b, int g, int qb_, int, int, int) {
+    const int64_t r = ((int64_t)b * p.Hkv + g) * p.Qb + qb_;
+    int start = __builtin_amdgcn_readfirstlane(p.indptr[r]);
+    int end = __builtin_amdgcn_readfirstlane(p.indptr[r + 1]);
+    start = start < 0 ? 0 : (start > p.nnz ? p.nnz : start);
+    end = end < start ? start : (end > p.nnz ? p.nnz : end);
+    row = p.indices + start;
+    n = end > start ? end - start : 0;
+    pos = 0;
+    qb = qb_;
+  }
+  __device__ bool next(int& id, bool& en) {
+    while (pos < n) {
+      const int v = __builtin_amdgcn_readfirstlane(row[pos]);
+      ++pos;
+      if (v >= 0 && v <= qb) {
+        id = v;
+        en = true;
+        return true;
+      }
+    }
+    return false;
+  }
+};
+
+template <>
+struct BlockIter<kModeMask> {
+  const uint8_t* base;  // row of the first head of the union
+  const uint8_t* own;   // row of this wave's head
+  int64_t hstride, cstride;
+  int nunion, qb, chunk, lane;
+  uint64_t bits, ownbits;
+  __device__ void init(const AttnParams& p, int b, int g, int qb_, int part, int hq, int lane_) {
+    cstride = p.ms[3];
+    qb = qb_;
+    lane = lane_;
+    chunk = 0;
+    bits = ownbits = 0;
+    if (p.mask_per_qhead) {
+      // Union over the query heads whose tiles this workgroup owns.
+      const int waves = blockDim.x >> 6;
+      const int t0 = part * waves;
+      int t1 = t0 + waves;
+      if (t1 > 2 * p.G) t1 = 2 * p.G;
+      const int h0 = t0 >> 1, h1 = (t1 - 1) >> 1;
+      base = p.mask + (int64_t)b * p.ms[0] + (int64_t)(g * p.G + h0) * p.ms[1] + (int64_t)qb_ * p.ms[2];
+      hstride = p.ms[1];
+      nunion = h1 - h0 + 1;
+      int oh = hq - h0;
+      if (oh < 0) oh = 0;
+      if (oh >= nunion) oh = nunion - 1;
+      own = base + (int64_t)oh * hstride;
+    } else {
+      base = p.mask + (int64_t)b * p.ms[0] + (int64_t)g * p.ms[1] + (int64_t)qb_ * p.ms[2];
+      hstride = 0;
+      nunion = 1;
+      own = base;
+    }
+  }
+  __device__ bool next(int& id, bool& en) {
+    while (bits == 0) {
+      if (chunk * 64 > qb) return false;
+      const int col = chunk * 64 + lane;
+      bool u = false, o = false;
+      if (col <= qb) {
+        for (int h = 0; h < nunion; ++h) u |= base[(int64_t)h * hstride + (int64_t)col * cstride] != 0;
+        o = own[(int64_t)col * cstride] != 0;
+      }
+      bits = __ballot(u);
+      ownbits = __ballot(o);
+      ++chunk;
+    }
+    const int pz = __builtin_ctzll(bits);
+    bits &= bits - 1;
+    id = (chunk - 1) * 64 + pz;
+    en = (ownbits >> pz) & 1;
+    return true;
+  }
+};
+
+// ------------------------------------------------------------------ kernel
+template <int D, int WAVES, typename TIn, bool F16, int MODE>
+__global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnParams p) {
+  constexpr int NTHR = WAVES * 64;
+  constexpr int KSTR = D + 8;        // K tile row stride, 16-bit elements (16 B pad)
+  constexpr int VSTR = kBlock + 8;   // V^T tile row stride
+  constexpr int KTILE = kBlock * KSTR;
+  constexpr int VTILE = D * VSTR;
+  constexpr int BUF = KTILE + VTILE;
+  constexpr int KROWCH = D / 8;                  // 16-byte chunks per K row
+  constexpr int KCHUNKS = kBlock * KROWCH;
+  constexpr int KCH = (KCHUNKS + NTHR - 1) / NTHR;
+  constexpr int VTASKS = (kBlock / 4) * (D / 8);  // 4 keys x 8 dims per task
+  constexpr int VTK = (VTASKS + NTHR - 1) / NTHR;
+  constexpr int DT = D / 32;  // 32-row tiles of O^T
+  constexpr int KS = D / 16;  // k-steps of S^T
+  constexpr int EB = TIn::bytes;
+
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * BUF];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hl = lane >> 5;
+
+  // ---- work item
+  const int roww = blockIdx.x / p.parts;
+  const int part = blockIdx.x - roww * p.parts;
+  int b, g, qb;
+  if (MODE == kModeCsr && p.row_order != nullptr) {
+    const int r = __builtin_amdgcn_readfirstlane(p.row_order[roww]);
+    if (r < 0 || r >= p.B * p.Hkv * p.Qb) return;  // uniform: before any barrier
+    qb = r % p.Qb;
+    const int bg = r / p.Qb;
+    g = bg % p.Hkv;
+    b = bg / p.Hkv;
+  } else {
+    // Heaviest (last) query blocks first: causal rows grow with qb.
+    const int bh = p.B * p.Hkv;
+    qb = p.Qb - 1 - roww / bh;
+    const int bg = roww - (roww / bh) * bh;
+    b = bg / p.Hkv;
+    g = bg - b * p.Hkv;
+  }
+  const int tile = part * WAVES + wave;
+  const bool active = tile < 2 * p.G;
+  const int hq = active ? (tile >> 1) : 0;
+  const int head = g * p.G + hq;
+  const int qin = (tile & 1) * 32 + l32;  // query row inside the 64-row block
+  const int qtok = qb * kBlock + qin;
+
+  // ---- Q fragment (B operand of S^T = K Q^T), resident for the whole row
+  uint4 qf[KS];
+  {
+    const char* qrow = static_cast<const char*>(p.q) +
+        ((int64_t)b * p.qs[0] + (int64_t)head * p.qs[1] + (int64_t)qtok * p.qs[2]) * EB;
+    const bool qv = active && qtok < p.T;
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk)
+      qf[kk] = load8<TIn, F16>(qrow + (int64_t)(16 * kk + 8 * hl) * EB, qv, p.qmul, p.prescale != 0);
+  }
+
+  const char* kbase = static_cast<const char*>(p.k) + ((int64_t)b * p.ks[0] + (int64_t)g * p.ks[1]) * EB;
+  const char* vbase = static_cast<const char*>(p.v) + ((int64_t)b * p.vs[0] + (int64_t)g * p.vs[1]) * EB;
+
+  raw8_t<TIn> kst[KCH];
+  raw8_t<TIn> vst[VTK][4];
+
+  auto load_block = [&](int blk) {
+    const int t0 = blk * kBlock;
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int c = tid + i * NTHR;
+      const int key = c / KROWCH, dc = c - (c / KROWCH) * KROWCH;
+      const bool ok = (c < KCHUNKS) && (t0 + key < p.T);
+      kst[i] = raw_load8<TIn>(kbase + ((int64_t)(t0 + key) * p.ks[2] + dc * 8) * EB, ok);
+    }
+#pragma unroll
+    for (int i = 0; i < VTK; ++i) {
+      const int t = tid + i * NTHR;
+      const int a = t & 15, bd = t >> 4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = 4 * a + j;
+        const bool ok = (t < VTASKS) && (t0 + key < p.T);
+        vst[i][j] = raw_load8<TIn>(vbase + ((int64_t)(t0 + key) * p.vs[2] + bd * 8) * EB, ok);
+      }
+    }
+  };
+
+  auto store_block = [&](int buf) {
+    uint16_t* Ks = smem + buf * BUF;
+    uint16_t* Vt = Ks + KTILE;
+#pragma unroll
+    for (int i = 0; i < KCH; ++i) {
+      const int c = tid + i * NTHR;
+      if (c < KCHUNKS) {
+        const int key = c / KROWCH, dc = c - (c / KROWCH) * KROWCH;
+        *reinterpret_cast<uint4*>(Ks + key * KSTR + dc * 8) = raw_to_mfma<TIn, F16>(kst[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VTK; ++i) {
+      const int t = tid + i * NTHR;
+      if (t < VTASKS) {
+        const int a = t & 15, bd = t >> 4;
+        const uint4 r0 = raw_to_mfma<TIn, F16>(vst[i][0]);
+        const uint4 r1 = raw_to_mfma<TIn, F16>(vst[i][1]);
+        const uint4 r2 = raw_to_mfma<TIn, F16>(vst[i][2]);
+        const uint4 r3 = raw_to_mfma<TIn, F16>(vst[i][3]);
+        const int pos = vt_pos(4 * a);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t w0 = elem16(r0, e) | (elem16(r1, e) << 16);
+          const uint32_t w1 = elem16(r2, e) | (elem16(r3, e) << 16);
+          *reinterpret_cast<uint2*>(Vt + (8 * bd + e) * VSTR + pos) = uint2{w0, w1};
+        }
+      }
+    }
+  };
+
+  float m_run = -INFINITY;  // running max of scaled scores (log2 domain)
+  float l_run = 0.f;        // running sum over this lane half's keys
+  f32x16_t acc[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16_t{};
+
+  auto compute = [&](int buf, bool diag) {
+    const uint16_t* Ks = smem + buf * BUF;
+    const uint16_t* Vt = Ks + KTILE;
+    f32x16_t s[2] = {f32x16_t{}, f32x16_t{}};
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      const uint4 a0 = *reinterpret_cast<const uint4*>(Ks + l32 * KSTR + 16 * kk + 8 * hl);
+      const uint4 a1 = *reinterpret_cast<const uint4*>(Ks + (32 + l32) * KSTR + 16 * kk + 8 * hl);
+      s[0] = mfma32x32x16<F16>(a0, qf[kk], s[0]);
+      s[1] = mfma32x32x16<F16>(a1, qf[kk], s[1]);
+    }
+    if (diag) {
+      // Accumulator register r of key tile c holds key 32c + 8(r/4) + 4(lane/32) + r%4.
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = 32 * c + 8 * (r >> 2) + 4 * hl + (r & 3);
+          if (key > qin) s[c][r] = -INFINITY;
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[c][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx * p.cs);
+    const float alpha = fast_exp2(m_run - m_new);
+    m_run = m_new;
+    float psum = 0.f;
+    uint4 pk[2][2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        uint32_t w[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x0 = fast_exp2(fmaf(s[c][8 * h2 + 2 * e], p.cs, -m_new));
+          const float x1 = fast_exp2(fmaf(s[c][8 * h2 + 2 * e + 1], p.cs, -m_new));
+          psum += x0 + x1;
+          w[e] = pack2<F16>(x0, x1);
+        }
+        pk[c][h2] = uint4{w[0], w[1], w[2], w[3]};
+      }
+    l_run = l_run * alpha + psum;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const uint4 a = *reinterpret_cast<const uint4*>(Vt + (dt * 32 + l32) * VSTR + 32 * c + 16 * h2 + 8 * hl);
+          acc[dt] = mfma32x32x16<F16>(a, pk[c][h2], acc[dt]);
+        }
+  };
+
+  BlockIter<MODE> it;
+  it.init(p, b, g, qb, part, hq, lane);
+  int cur_id = 0;
+  bool cur_en = false;
+  if (it.next(cur_id, cur_en)) {
+    load_block(cur_id);
+    store_block(0);
+    __syncthreads();
+    int buf = 0;
+    while (true) {
+      int nid = 0;
+      bool nen = false;
+      const bool more = it.next(nid, nen);
+      if (more) load_block(nid);
+      if (active && cur_en) compute(buf, cur_id == qb);
+      if (!more) break;
+      store_block(buf ^ 1);
+      __syncthreads();
+      buf ^= 1;
+      cur_id = nid;
+      cur_en = nen;
+    }
+  }
+
+  if (!active) return;
+  const float lt = l_run + __shfl_xor(l_run, 32);
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  if (qtok >= p.T) return;
+  char* orow = static_cast<char*>(p.o) +
+      ((int64_t)b * p.os[0] + (int64_t)head * p.os[1] + (int64_t)qtok * p.os[2]) * EB;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int d = dt * 32 + 8 * j + 4 * hl;
+      const float o0 = acc[dt][4 * j] * inv, o1 = acc[dt][4 * j + 1] * inv;
+      const float o2 = acc[dt][4 * j + 2] * inv, o3 = acc[dt][4 * j + 3] * inv;
+      if constexpr (EB == 2) {
+        *reinterpret_cast<uint2*>(orow + (int64_t)d * EB) = uint2{pack2<F16>(o0, o1), pack2<F16>(o2, o3)};
+      } else {
+        *reinterpret_cast<float4*>(orow + (int64_t)d * EB) = float4{o0, o1, o2, o3};
+      }
+    }
+}
+
+// ------------------------------------------------------------------ launch
+struct LaunchShape {
+  int waves;
+  int parts;
+};
+
+// Tiles of one (batch, KV head, query block) row: 2 per query head.  Prefer
+// the widest workgroup (up to 8 waves) that divides them evenly, so every
+// wave has a tile and the row's K/V blocks are fetched as few times as possible.
+inline LaunchShape choose_shape(int variant, int G) {
+  const int tiles = 2 * G;
+  if (variant == SPRUCE_VARIANT_SINGLE_HEAD_QTILE) return {2, G};
+  const int opts[4] = {8, 7, 4, 2};
+  for (int w : opts)
+    if (tiles % w == 0) return {w, tiles / w};
+  return {4, (tiles + 3) / 4};
+}
+
+template <int D, int WAVES, typename TIn, bool F16, int MODE>
+int launch_attention_t(const AttnParams& p, hipStream_t stream) {
+  const int64_t grid = (int64_t)p.B * p.Hkv * p.Qb * p.parts;
+  hipLaunchKernelGGL((sparse_prefill_kernel<D, WAVES, TIn, F16, MODE>), dim3((unsigned)grid),
+                     dim3(WAVES * 64), 0, stream, p);
+  return check_launch("sparse_prefill_kernel");
+}
+
+template <int MODE, int D, typename TIn, bool F16>
+int launch_attention_w(const AttnParams& p, int waves, hipStream_t stream) {
+  switch (waves) {
+    case 2: return launch_attention_t<D, 2, TIn, F16, MODE>(p, stream);
+    case 4: return launch_attention_t<D, 4, TIn, F16, MODE>(p, stream);
+    case 7: return launch_attention_t<D, 7, TIn, F16, MODE>(p, stream);
+    case 8: return launch_attention_t<D, 8, TIn, F16, MODE>(p, stream);
+    default: return set_error(SPRUCE_EINVAL, "unsupported wave count %d", waves);
+  }
+}
+
+template <int MODE>
+int launch_attention(const AttnParams& p, int D, int dtype, int waves, hipStream_t stream) {
+  if (D == 128) {
+    if (dtype == SPRUCE_DTYPE_BF16) return launch_attention_w<MODE, 128, InBF16, false>(p, waves, stream);
+    if (dtype == SPRUCE_DTYPE_F16) return launch_attention_w<MODE, 128, InF16, true>(p, waves, stream);
+    return launch_attention_w<MODE, 128, InF32, false>(p, waves, stream);
+  }
+  if (dtype == SPRUCE_DTYPE_BF16) return launch_attention_w<MODE, 64, InBF16, false>(p, waves, stream);
+  if (dtype == SPRUCE_DTYPE_F16) return launch_attention_w<MODE, 64, InF16, true>(p, waves, stream);
+  return launch_attention_w<MODE, 64, InF32, false>(p, waves, stream);
+}
+
+// Shared argument checks and parameter setup of the three entry points.
+int prepare_attention(AttnParams& p, const void* q, const int64_t qs[4], const void* k,
+                      const int64_t ks[4], const void* v, const int64_t vs[4], int64_t B,
+                      int64_t Hq, int64_t Hkv, int64_t T, int64_t D, float scale, int dtype,
+                      int variant, void* out, const int64_t os[4], LaunchShape& shape);
+
+}  // namespace spruce

@@ -1,0 +1,146 @@
+"""Direct-index block-sparse causal GQA prefill on gfx950 (HIP, C ABI).
+
+Host side of ``spruce_sparse_prefill_index`` / ``spruce_sparse_prefill_csr``.
+It mirrors the reference's ``direct_index_sparse_triton``
+(kernels/seerattention_direct_index_triton.py:339-416): the same argument
+meaning, validation order, exception types and output layout -- q is
+``[B,Hq,T,D]`` (any strides with a contiguous last dim, e.g. the transposed
+view of Qwen's ``[B,T,Hq,D]`` projection), k/v and indices stay at KV-head
+resolution, and the output is a contiguous ``[B,T,Hq,D]`` tensor written
+through logical ``[B,Hq,T,D]`` strides.
+"""
+import torch
+
+import spruce_hip
+from spruce_hip import KERNEL_VARIANTS
+
+_LAST_CONFIG = {}
+
+
+def _check_common(q, k, v, block_size, kernel_variant):
+    if kernel_variant not in KERNEL_VARIANTS:
+        raise ValueError(
+            f"kernel_variant must be one of {KERNEL_VARIANTS}, "
+            f"got {kernel_variant!r}")
+    if not q.is_cuda:
+        raise RuntimeError("the direct-index HIP backend requires GPU tensors")
+    if block_size != 64:
+        raise ValueError("direct-index kernel currently supports block_size=64 only")
+    if k.shape != v.shape or q.shape[0] != k.shape[0] or q.shape[2:] != k.shape[2:]:
+        raise ValueError("q and k/v must match in batch, tokens, and head_dim")
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise ValueError("q, k and v must share one dtype")
+    if k.device != q.device or v.device != q.device:
+        raise ValueError("q, k and v must be on the same device")
+    B, Hq, T, D = q.shape
+    Hkv = k.shape[1]
+    if Hq % Hkv:
+        raise ValueError("query heads must be divisible by KV heads")
+    if D not in (64, 128):
+        raise ValueError(f"kernel supports head_dim 64 or 128, got {D}")
+    return B, Hq, Hkv, T, D
+
+
+def _output(q):
+    B, Hq, T, D = q.shape
+    out = torch.empty((B, T, Hq, D), device=q.device, dtype=q.dtype)
+    # Logical [B,Hq,T,D] strides over the contiguous [B,T,Hq,D] storage.
+    return out, spruce_hip.strides(out, order=(0, 2, 1, 3))
+
+
+def _record(kernel_variant, Hq, Hkv, D):
+    _LAST_CONFIG[kernel_variant] = spruce_hip.launch_config(
+        kernel_variant, Hq, Hkv, D)["best_config"]
+
+
+def direct_index_sparse_prefill(q, k, v, indices, scale, block_size=64,
+                                kernel_variant="single_head"):
+    """Causal block-sparse attention over exactly the supplied block IDs.
+
+    indices: int32 ``[B,Hkv,ceil(T/64),K]``; negative entries are padding.
+    Returns ``[B,T,Hq,D]`` in q's dtype.
+    """
+    B, Hq, Hkv, T, D = _check_common(q, k, v, block_size, kernel_variant)
+    qblocks = (T + block_size - 1) // block_size
+    if tuple(indices.shape[:3]) != (B, Hkv, qblocks) or indices.dtype != torch.int32:
+        raise ValueError("indices must be int32 [B,Hkv,ceil(T/64),K]")
+    if indices.dim() != 4:
+        raise ValueError("indices must be int32 [B,Hkv,ceil(T/64),K]")
+    if any(x.stride(-1) != 1 for x in (q, k, v, indices)):
+        raise ValueError("q, k, v, and indices must have a contiguous final dimension")
+    if indices.device != q.device:
+        raise ValueError("indices must be on the same device as q")
+    out, out_strides = _output(q)
+    with torch.cuda.device(q.device):
+        rc = spruce_hip.lib().spruce_sparse_prefill_index(
+            spruce_hip.ptr(q), spruce_hip.strides(q),
+            spruce_hip.ptr(k), spruce_hip.strides(k),
+            spruce_hip.ptr(v), spruce_hip.strides(v),
+            spruce_hip.ptr(indices), spruce_hip.strides(indices), indices.shape[3],
+            B, Hq, Hkv, T, D, float(scale), spruce_hip.dtype_code(q),
+            spruce_hip.variant_code(kernel_variant),
+            spruce_hip.ptr(out), out_strides, spruce_hip.stream_of(q))
+    spruce_hip.check(rc, "spruce_sparse_prefill_index")
+    _record(kernel_variant, Hq, Hkv, D)
+    return out
+
+
+def direct_index_sparse_csr(q, k, v, indptr, indices, scale, block_size=64,
+                            row_order=None, kernel_variant="single_head"):
+    """Causal block-sparse attention over variable-length (CSR) block lists.
+
+    Row ``r = (b*Hkv + kv_head)*Qb + query_block`` attends the key blocks
+    ``indices[indptr[r]:indptr[r+1]]``.  ``row_order`` (int32 permutation of
+    the rows, optional) sets the dispatch order; heaviest rows first balances
+    variable row lengths.  Returns ``[B,T,Hq,D]`` in q's dtype.
+    """
+    B, Hq, Hkv, T, D = _check_common(q, k, v, block_size, kernel_variant)
+    qblocks = (T + block_size - 1) // block_size
+    rows = B * Hkv * qblocks
+    if indptr.dtype != torch.int32 or indices.dtype != torch.int32:
+        raise ValueError("indptr and indices must be int32")
+    if indptr.dim() != 1 or indptr.numel() != rows + 1:
+        raise ValueError(f"indptr must be 1-D with B*Hkv*ceil(T/64)+1 = {rows + 1} entries")
+    if not indptr.is_contiguous() or not indices.is_contiguous():
+        raise ValueError("indptr and indices must be contiguous")
+    if any(x.stride(-1) != 1 for x in (q, k, v)):
+        raise ValueError("q, k, and v must have a contiguous final dimension")
+    if row_order is not None:
+        if row_order.dtype != torch.int32 or row_order.numel() != rows or not row_order.is_contiguous():
+            raise ValueError(f"row_order must be a contiguous int32 permutation of {rows} rows")
+    for t in (indptr, indices) + ((row_order,) if row_order is not None else ()):
+        if t.device != q.device:
+            raise ValueError("index tensors must be on the same device as q")
+    out, out_strides = _output(q)
+    with torch.cuda.device(q.device):
+        rc = spruce_hip.lib().spruce_sparse_prefill_csr(
+            spruce_hip.ptr(q), spruce_hip.strides(q),
+            spruce_hip.ptr(k), spruce_hip.strides(k),
+            spruce_hip.ptr(v), spruce_hip.strides(v),
+            spruce_hip.ptr(indptr), spruce_hip.ptr(indices), indices.numel(),
+            spruce_hip.ptr(row_order),
+            B, Hq, Hkv, T, D, float(scale), spruce_hip.dtype_code(q),
+            spruce_hip.variant_code(kernel_variant),
+            spruce_hip.ptr(out), out_strides, spruce_hip.stream_of(q))
+    spruce_hip.check(rc, "spruce_sparse_prefill_csr")
+    _record(kernel_variant, Hq, Hkv, D)
+    return out
+
+
+def csr_row_order(indptr):
+    """Dispatch order heaviest-row-first (longest processing time first)."""
+    counts = indptr[1:] - indptr[:-1]
+    return torch.argsort(counts, descending=True, stable=True).to(torch.int32)
+
+
+def kernel_runtime_metadata(kernel_variant):
+    """Return the launch configuration of the most recent call of a variant.
+
+    Mirrors kernels/seerattention_direct_index_triton.py:430-447: ``best_config``
+    is None until the variant has run once in this process.
+    """
+    if kernel_variant not in KERNEL_VARIANTS:
+        raise ValueError(
+            f"kernel_variant must be one of {KERNEL_VARIANTS}, "
+            f"got {kernel_variant!r}")
+    return {"variant": kernel_variant, "best_config": _LAST_CONFIG.get(kernel_variant)}

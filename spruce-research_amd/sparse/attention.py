@@ -1,0 +1,148 @@
+"""Block-sparse prefill attention entry point for Hugging Face models (HIP).
+
+Drop-in for the reference's sparse/attention.py: ``SPARSE_PREFILL_ATTENTION``,
+``sparse_prefill_attention_forward`` with the same signature, validation
+messages and exception types (sparse/attention.py:119-190, 276-289), and
+``register_sparse_prefill_attention``.  The reference computes this with a
+host loop of small PyTorch ops; here the whole layer is one launch of the
+gfx950 direct-index kernel, which reads ``selected_blocks[:, layer_idx]`` in
+place.
+
+Differences, all raising instead of computing something else:
+  * ``block_size`` must be 64 and ``head_dim`` 64 or 128 (the kernel's tile);
+  * ``attention_mask`` must be None (B=1 unpadded prefill; causality is
+    applied by the kernel), as in the reference's kernel backend;
+  * ``residual_summaries=True`` raises NotImplementedError.
+"""
+import math
+from typing import Optional
+
+import torch
+
+from interfaces.validator import validate_selected_blocks
+from kernels.direct_index import direct_index_sparse_prefill
+
+SPARSE_PREFILL_ATTENTION = "spruce_sparse_prefill"
+SUMMARY_PROTOTYPES = (1, 2, 4)
+SUMMARY_MODES = ("mean", "learned")
+
+
+def _layer_index(module: torch.nn.Module) -> int:
+    for name in ("layer_idx", "layer_id"):
+        value = getattr(module, name, None)
+        if value is not None:
+            return int(value)
+    raise ValueError(
+        "Sparse prefill attention needs module.layer_idx (or module.layer_id) "
+        "to select the correct selected_blocks layer."
+    )
+
+
+def _validate_inputs(query, key, value, selected_blocks, block_size, layer_idx, validate_blocks):
+    """Shape checks of sparse/attention.py:131-170, same messages."""
+    if query.dim() != 4 or key.dim() != 4 or value.dim() != 4:
+        raise ValueError("query, key, and value must be [batch, heads, tokens, head_dim]")
+    if key.shape != value.shape:
+        raise ValueError(f"key/value shape mismatch: {tuple(key.shape)} vs {tuple(value.shape)}")
+    if query.shape[0] != key.shape[0] or query.shape[-1] != key.shape[-1]:
+        raise ValueError("query and key must have the same batch size and head dimension")
+    if query.shape[-2] != key.shape[-2]:
+        raise ValueError(
+            "Stage 3.2 is prefill-only: query and key lengths must match "
+            f"(got {query.shape[-2]} and {key.shape[-2]})."
+        )
+    if block_size < 1:
+        raise ValueError(f"block_size must be positive, got {block_size}")
+    if query.shape[1] % key.shape[1]:
+        raise ValueError(
+            f"query heads ({query.shape[1]}) must be divisible by KV heads ({key.shape[1]})")
+    if validate_blocks:
+        validate_selected_blocks(selected_blocks)
+    batch, layers, groups, query_blocks, _ = selected_blocks.shape
+    expected_blocks = math.ceil(query.shape[-2] / block_size)
+    if batch != query.shape[0] or layers <= layer_idx:
+        raise ValueError(
+            f"selected_blocks shape {tuple(selected_blocks.shape)} does not cover "
+            f"batch {query.shape[0]} and layer {layer_idx}")
+    if groups != key.shape[1]:
+        raise ValueError(
+            f"selected_blocks has {groups} KV groups, model has {key.shape[1]} KV heads")
+    if query_blocks != expected_blocks:
+        raise ValueError(
+            f"selected_blocks has {query_blocks} query blocks; expected {expected_blocks} "
+            f"for seq_len={query.shape[-2]} and block_size={block_size}")
+
+
+def sparse_prefill_attention_forward(
+    module: torch.nn.Module,
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    attention_mask: Optional[torch.Tensor],
+    *,
+    selected_blocks: torch.Tensor,
+    block_size: int,
+    validate_selected_blocks_input: bool = True,
+    residual_summaries: bool = False,
+    residual_summary_nodes: Optional[torch.Tensor] = None,
+    summary_prototypes: int = 1,
+    summary_mode: str = "mean",
+    summary_checkpoint: Optional[str] = None,
+    validate_residual_summary_nodes_input: bool = True,
+    **kwargs,
+) -> tuple[torch.Tensor, None]:
+    """Transformers AttentionInterface implementation for sparse prefill.
+
+    query ``[B,Hq,T,D]``, key/value ``[B,Hkv,T,D]``, ``selected_blocks``
+    ``[B,L,Hkv,ceil(T/block_size),K]`` int32.  Returns ``([B,T,Hq,D], None)``.
+    """
+    del kwargs
+    layer_idx = _layer_index(module)
+    _validate_inputs(query, key, value, selected_blocks, block_size, layer_idx,
+                     validate_blocks=validate_selected_blocks_input)
+    if summary_prototypes not in SUMMARY_PROTOTYPES:
+        raise ValueError(
+            f"summary_prototypes must be one of {SUMMARY_PROTOTYPES}, got {summary_prototypes}")
+    if summary_mode not in SUMMARY_MODES:
+        raise ValueError(f"summary_mode must be one of {SUMMARY_MODES}, got {summary_mode!r}")
+    if residual_summaries:
+        raise NotImplementedError(
+            "residual summaries are not implemented in the HIP sparse-prefill path")
+    if attention_mask is not None:
+        if attention_mask.dim() != 4:
+            raise ValueError(
+                "Sparse prefill expects the Transformers 4D additive attention mask; "
+                f"got shape {tuple(attention_mask.shape)}")
+        raise ValueError(
+            "the HIP sparse-prefill path applies causality itself and supports "
+            "attention_mask=None only (unpadded prefill)")
+    if block_size != 64:
+        raise ValueError("the HIP sparse-prefill kernel requires block_size=64")
+    indices = selected_blocks[:, layer_idx].to(device=query.device, dtype=torch.int32).contiguous()
+    # The reference raises on a row with no selected block (sparse/attention.py:284-289).
+    empty = ~(indices >= 0).any(dim=-1)
+    if bool(empty.any()):
+        b, g, qb = (int(x) for x in torch.nonzero(empty)[0])
+        raise ValueError(
+            "selected_blocks leaves an attention row empty at "
+            f"batch={b}, layer={layer_idx}, kv_head={g}, query_block={qb}")
+    D = query.shape[-1]
+    output = direct_index_sparse_prefill(
+        query, key, value, indices, scale=1.0 / math.sqrt(D), block_size=block_size)
+    return output, None
+
+
+def register_sparse_prefill_attention(name: str = SPARSE_PREFILL_ATTENTION) -> str:
+    """Register this backend with Transformers (sparse/attention.py:367-382).
+
+    Prefill receives no O(T^2) mask (the kernel is causal by construction);
+    decode keeps SDPA's mask.
+    """
+    try:
+        from transformers import AttentionInterface, AttentionMaskInterface
+    except ImportError as error:
+        raise RuntimeError("register_sparse_prefill_attention requires transformers") from error
+    from kernels.sparse_prefill import _triton_attention_mask
+    AttentionInterface.register(name, sparse_prefill_attention_forward)
+    AttentionMaskInterface.register(name, _triton_attention_mask)
+    return name

@@ -1,0 +1,77 @@
+"""The C ABI library: it loads, exports every symbol include/*.h declares, and
+rejects invalid arguments with SPRUCE_EINVAL before touching the GPU (so these
+run on a machine without one)."""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+import spruce_hip
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_functions():
+    names = set()
+    for header in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = open(header).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names.update(re.findall(r"\b(spruce_\w+)\s*\(", text))
+    return sorted(names)
+
+
+def test_library_is_built_and_exports_every_declared_symbol():
+    assert spruce_hip.is_built(), "run __graft_entry__.build() first"
+    lib = ctypes.CDLL(spruce_hip.LIB_PATH)
+    declared = _declared_functions()
+    assert "spruce_sparse_prefill_index" in declared
+    missing = [n for n in declared if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_version_string():
+    assert "gfx950" in spruce_hip.version()
+
+
+def _strides(*s):
+    return (ctypes.c_int64 * 4)(*s)
+
+
+def _call_index(D=128, Hq=4, Hkv=2, dtype=0, variant=0, qs=(0, 0, 128, 1), K=1, null_idx=False):
+    lib = spruce_hip.lib()
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: validation fails first
+    return lib.spruce_sparse_prefill_index(
+        fake, _strides(*qs), fake, _strides(0, 0, 128, 1), fake, _strides(0, 0, 128, 1),
+        None if null_idx else fake, _strides(0, 0, 1, 1), K,
+        1, Hq, Hkv, 64, D, 0.1, dtype, variant, fake, _strides(0, 128, 512, 1), None)
+
+
+@pytest.mark.parametrize("kwargs, message", [
+    (dict(D=96), "head_dim 64 or 128"),
+    (dict(Hq=3, Hkv=2), "divisible"),
+    (dict(dtype=7), "dtype"),
+    (dict(variant=9), "variant"),
+    (dict(qs=(0, 0, 128, 2)), "contiguous final dimension"),
+    (dict(qs=(0, 0, 100, 1)), "16-byte aligned"),
+    (dict(null_idx=True), "indices"),
+])
+def test_invalid_arguments_return_einval_with_message(kwargs, message):
+    rc = _call_index(**kwargs)
+    assert rc == -1
+    assert message in spruce_hip.last_error()
+
+
+def test_error_codes_map_to_reference_exception_types():
+    assert _call_index(D=96) == -1
+    with pytest.raises(ValueError, match="head_dim"):
+        spruce_hip.check(-1, "spruce_sparse_prefill_index")
+
+
+def test_kernel_metadata_reports_launch_shape():
+    cfg = spruce_hip.launch_config("single_head", 28, 4, 128)
+    assert cfg["variant"] == "single_head"
+    best = cfg["best_config"]
+    assert best["waves_per_workgroup"] * best["workgroups_per_row"] == 14  # 7 heads x 2 tiles
+    assert spruce_hip.launch_config("single_head_prescale", 8, 2, 64)["best_config"]["prescale_q"]

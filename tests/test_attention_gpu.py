@@ -1,0 +1,269 @@
+"""Parity of the gfx950 sparse-prefill kernels (through the C ABI) with the
+CPU oracle on identical seeded inputs.
+
+Bar (north star): max-abs error <= 2e-2 and mean-abs error <= 1e-3 against
+the float32 oracle; the reference's own Triton parity cases additionally use
+its torch.testing tolerance atol = rtol = 2e-2
+(tests/test_triton_sparse_prefill.py:94,125 in the reference).  Full-size
+configurations are spot-checked on sampled query blocks and through
+size-independent properties: the three list layouts and the dispatch order
+give bit-identical outputs for identical block sets.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle.attention as ora
+from kernels.block_mask import block_sparse_prefill
+from kernels.direct_index import (
+    KERNEL_VARIANTS,
+    csr_row_order,
+    direct_index_sparse_csr,
+    direct_index_sparse_prefill,
+    kernel_runtime_metadata,
+)
+from kernels.sparse_prefill import triton_sparse_prefill_attention_forward
+from sparse.attention import sparse_prefill_attention_forward
+from spruce_hip import workloads
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+MAX_ABS, MEAN_ABS = 2e-2, 1e-3
+
+
+class _Module(torch.nn.Module):
+    layer_idx = 0
+
+
+def _err(actual, expected):
+    a = actual.detach().float().cpu().numpy().astype(np.float64)
+    d = np.abs(a - np.asarray(expected, dtype=np.float64))
+    return float(d.max()), float(d.mean())
+
+
+def _assert_parity(actual, expected, max_abs=MAX_ABS, mean_abs=MEAN_ABS, what=""):
+    mx, mn = _err(actual, expected)
+    print(f"{what}: max_abs={mx:.3e} mean_abs={mn:.3e}", flush=True)
+    assert np.isfinite(actual.float().cpu().numpy()).all(), what
+    assert mx <= max_abs and mn <= mean_abs, (what, mx, mn)
+
+
+def _bthd(B, T, H, D, dtype, gen):
+    """Qwen projection layout: contiguous [B,T,H,D] viewed as [B,H,T,D]."""
+    return torch.randn(B, T, H, D, generator=gen).to(dtype).transpose(1, 2)
+
+
+@pytest.mark.parametrize("variant", KERNEL_VARIANTS)
+def test_reference_parity_case_one_block(variant):
+    # Reference tests/test_triton_sparse_prefill.py:74-95 (fp16, strided views).
+    torch.manual_seed(0)
+    q = torch.randn(1, 64, 2, 64, dtype=torch.float16).transpose(1, 2)
+    k = torch.randn(1, 64, 1, 64, dtype=torch.float16).transpose(1, 2)
+    v = torch.randn(1, 64, 1, 64, dtype=torch.float16).transpose(1, 2)
+    assert not q.is_contiguous()
+    selected = torch.zeros((1, 1, 1, 1, 1), dtype=torch.int32)
+    expected = ora.sparse_attention_index(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                          selected[:, 0].numpy())
+    qd, kd, vd = (x.transpose(1, 2).contiguous().to(DEV).transpose(1, 2) for x in (q, k, v))
+    actual, _ = triton_sparse_prefill_attention_forward(
+        _Module(), qd, kd, vd, None, selected_blocks=selected.to(DEV), block_size=64,
+        kernel_variant=variant)
+    assert actual.shape == (1, 64, 2, 64) and actual.is_contiguous()
+    torch.testing.assert_close(actual.float().cpu(), torch.from_numpy(expected), atol=2e-2, rtol=2e-2)
+    assert kernel_runtime_metadata(variant)["best_config"] is not None
+
+
+@pytest.mark.parametrize("variant", KERNEL_VARIANTS)
+def test_reference_parity_case_across_blocks(variant):
+    # Reference tests/test_triton_sparse_prefill.py:103-125.
+    torch.manual_seed(4)
+    q = torch.randn(1, 128, 4, 64, dtype=torch.float16).transpose(1, 2)
+    k = torch.randn(1, 128, 2, 64, dtype=torch.float16).transpose(1, 2)
+    v = torch.randn(1, 128, 2, 64, dtype=torch.float16).transpose(1, 2)
+    selected = torch.tensor([[[[[0, -1], [0, 1]], [[0, -1], [0, 1]]]]], dtype=torch.int32)
+    expected = ora.sparse_attention_index(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                          selected[:, 0].numpy())
+    qd, kd, vd = (x.transpose(1, 2).contiguous().to(DEV).transpose(1, 2) for x in (q, k, v))
+    actual, _ = triton_sparse_prefill_attention_forward(
+        _Module(), qd, kd, vd, None, selected_blocks=selected.to(DEV), block_size=64,
+        kernel_variant=variant)
+    torch.testing.assert_close(actual.float().cpu(), torch.from_numpy(expected), atol=2e-2, rtol=2e-2)
+
+
+def test_cfg1_block_mask_fp32_inputs():
+    # BASELINE cfg1: T=4096, 8q/2kv, d=128, fp32 N(0,1), top-16 + sink + diagonal.
+    q, k, v = workloads.qkv(0, 4096, 8, 2, 128, torch.float32, use_rope=False)
+    mask = workloads.cfg1_mask(0)
+    expected = ora.sparse_attention_mask(q.numpy(), k.numpy(), v.numpy(), mask.numpy())
+    actual = block_sparse_prefill(q.to(DEV), k.to(DEV), v.to(DEV), mask.to(DEV), scale=128 ** -0.5)
+    _assert_parity(actual.transpose(1, 2), expected, what="cfg1 mask fp32")
+
+
+def _messy_index_rows(rng, B, Hkv, qblocks, K):
+    idx = np.full((B, Hkv, qblocks, K), -1, np.int32)
+    for b in range(B):
+        for g in range(Hkv):
+            for qb in range(qblocks):
+                n = rng.integers(0, K + 1)
+                row = list(rng.integers(-1, qblocks + 2, size=n))   # -1, dups, future ids
+                if rng.random() < 0.8:
+                    row.append(qb)
+                row = row[:K]
+                rng.shuffle(row)
+                idx[b, g, qb, : len(row)] = row
+    return idx
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,T,D,dtype", [
+    (2, 14, 2, 1000, 128, torch.bfloat16),   # G=7, ragged last block
+    (1, 8, 2, 777, 64, torch.float16),       # G=4, D=64
+    (1, 3, 3, 300, 128, torch.float32),      # G=1, fp32 inputs
+    (1, 12, 2, 640, 128, torch.bfloat16),    # G=6 (Qwen2.5-1.5B grouping)
+])
+def test_direct_index_messy_rows(B, Hq, Hkv, T, D, dtype):
+    rng = np.random.default_rng(B * 1000 + Hq * 10 + D)
+    gen = torch.Generator().manual_seed(int(T))
+    q = _bthd(B, T, Hq, D, dtype, gen)
+    k = _bthd(B, T, Hkv, D, dtype, gen)
+    v = _bthd(B, T, Hkv, D, dtype, gen)
+    qblocks = (T + 63) // 64
+    idx = _messy_index_rows(rng, B, Hkv, qblocks, 6)
+    expected = ora.sparse_attention_index(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                          idx, empty="zero")
+    dev = [x.transpose(1, 2).contiguous().to(DEV).transpose(1, 2) for x in (q, k, v)]
+    actual = direct_index_sparse_prefill(*dev, torch.from_numpy(idx).to(DEV), scale=D ** -0.5)
+    _assert_parity(actual, expected, what=f"index B{B} Hq{Hq} Hkv{Hkv} T{T} D{D} {dtype}")
+
+
+@pytest.mark.parametrize("variant", ["single_head_qtile", "single_head_prescale", "tiled_gqa"])
+def test_variants_agree_with_oracle(variant):
+    gen = torch.Generator().manual_seed(17)
+    q = _bthd(1, 512, 28, 128, torch.bfloat16, gen)
+    k = _bthd(1, 512, 4, 128, torch.bfloat16, gen)
+    v = _bthd(1, 512, 4, 128, torch.bfloat16, gen)
+    idx = torch.tensor([[[[0, q_, -1] if q_ else [0, -1, -1] for q_ in range(8)]] * 4], dtype=torch.int32)
+    expected = ora.sparse_attention_index(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                          idx.numpy())
+    dev = [x.transpose(1, 2).contiguous().to(DEV).transpose(1, 2) for x in (q, k, v)]
+    actual = direct_index_sparse_prefill(*dev, idx.to(DEV), scale=128 ** -0.5, kernel_variant=variant)
+    _assert_parity(actual, expected, what=variant)
+
+
+def test_csr_rows_with_row_order_and_empty_rows():
+    rng = np.random.default_rng(23)
+    B, Hq, Hkv, T, D = 1, 8, 2, 700, 64
+    gen = torch.Generator().manual_seed(3)
+    q = _bthd(B, T, Hq, D, torch.float16, gen)
+    k = _bthd(B, T, Hkv, D, torch.float16, gen)
+    v = _bthd(B, T, Hkv, D, torch.float16, gen)
+    qblocks = (T + 63) // 64
+    rows = []
+    for _ in range(B * Hkv * qblocks):
+        rows.append(rng.integers(-1, qblocks, size=rng.integers(0, 9)).astype(np.int32))
+    indptr = np.concatenate([[0], np.cumsum([r.size for r in rows])]).astype(np.int32)
+    indices = np.concatenate(rows).astype(np.int32)
+    expected = ora.sparse_attention_csr(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                        indptr, indices, empty="zero")
+    dev = [x.transpose(1, 2).contiguous().to(DEV).transpose(1, 2) for x in (q, k, v)]
+    ip, ix = torch.from_numpy(indptr).to(DEV), torch.from_numpy(indices).to(DEV)
+    plain = direct_index_sparse_csr(*dev, ip, ix, scale=D ** -0.5)
+    ordered = direct_index_sparse_csr(*dev, ip, ix, scale=D ** -0.5, row_order=csr_row_order(ip))
+    _assert_parity(plain, expected, what="csr")
+    assert torch.equal(plain, ordered)
+
+
+def test_mask_per_query_head_and_per_kv_head():
+    rng = np.random.default_rng(31)
+    B, Hq, Hkv, T, D = 1, 8, 2, 512, 128
+    gen = torch.Generator().manual_seed(5)
+    q = torch.randn(B, Hq, T, D, generator=gen).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, T, D, generator=gen).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, T, D, generator=gen).to(torch.bfloat16)
+    qblocks = T // 64
+    per_q = rng.random((B, Hq, qblocks, qblocks)) < 0.4   # heads of a group differ
+    per_q[0, 1, 3] = False                                 # one empty (head, row): zeros
+    per_kv = rng.random((B, Hkv, qblocks, qblocks)) < 0.4
+    for m in (per_q, per_kv):
+        expected = ora.sparse_attention_mask(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                             m, empty="zero")
+        actual = block_sparse_prefill(q.to(DEV), k.to(DEV), v.to(DEV), torch.from_numpy(m).to(DEV),
+                                      scale=D ** -0.5)
+        _assert_parity(actual.transpose(1, 2), expected, what=f"mask heads={m.shape[1]}")
+
+
+def test_reference_shaped_mask_call_with_expanded_kv():
+    # The reference kernel requires q.shape == k.shape (GQA pre-expanded).
+    gen = torch.Generator().manual_seed(8)
+    q = torch.randn(1, 4, 256, 64, generator=gen).to(torch.float16)
+    k = torch.randn(1, 4, 256, 64, generator=gen).to(torch.float16)
+    v = torch.randn(1, 4, 256, 64, generator=gen).to(torch.float16)
+    mask = torch.tril(torch.ones(4, 4, dtype=torch.bool))[None, None].expand(1, 4, 4, 4).contiguous()
+    expected = ora.dense_causal_attention(q.float().numpy(), k.float().numpy(), v.float().numpy())
+    actual = block_sparse_prefill(q.to(DEV), k.to(DEV), v.to(DEV), mask.to(DEV), scale=64 ** -0.5)
+    _assert_parity(actual.transpose(1, 2), expected, what="all-causal mask == dense")
+
+
+def test_sparse_attention_entry_point_drop_in():
+    gen = torch.Generator().manual_seed(2)
+    q = _bthd(1, 256, 4, 128, torch.bfloat16, gen)
+    k = _bthd(1, 256, 2, 128, torch.bfloat16, gen)
+    v = _bthd(1, 256, 2, 128, torch.bfloat16, gen)
+    rows = [[0, -1], [0, 1], [1, 2], [2, 3]]
+    sel = torch.tensor([[[rows, rows]]], dtype=torch.int32)   # [B=1, L=1, Hkv=2, Qb=4, K=2]
+    expected = ora.sparse_attention_index(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                          sel[:, 0].numpy())
+    dev = [x.transpose(1, 2).contiguous().to(DEV).transpose(1, 2) for x in (q, k, v)]
+    actual, w = sparse_prefill_attention_forward(_Module(), *dev, None, selected_blocks=sel.to(DEV),
+                                                 block_size=64)
+    assert w is None
+    _assert_parity(actual, expected, what="sparse/attention.py")
+    bad = sel.clone()
+    bad[0, 0, 1, 2] = -1
+    with pytest.raises(ValueError, match="row empty"):
+        sparse_prefill_attention_forward(_Module(), *dev, None, selected_blocks=bad.to(DEV),
+                                         block_size=64, validate_selected_blocks_input=False)
+
+
+def test_full_size_cfg2_sampled_rows_and_layout_identity():
+    # BASELINE cfg2 at full size: T=32768, 28q/4kv, bf16 + RoPE, ~10% density.
+    print("cfg2: generating inputs", flush=True)
+    q, k, v = workloads.qkv(0, 32768, 28, 4, 128, torch.bfloat16, use_rope=True, layout="bthd")
+    mask, density = workloads.cfg2_mask(0)
+    assert 0.09 < density < 0.12
+    dev = [x.transpose(1, 2).contiguous().to(DEV).transpose(1, 2) for x in (q, k, v)]
+    mask_d = mask.to(DEV)
+    by_mask = block_sparse_prefill(*dev, mask_d, scale=128 ** -0.5)
+    sel = workloads.mask_to_selected_blocks(mask[:, ::7]).to(DEV)
+    by_index = direct_index_sparse_prefill(*dev, sel, scale=128 ** -0.5)
+    torch.cuda.synchronize()
+    # Same blocks in the same ascending order -> bit-identical results.
+    assert torch.equal(by_mask.transpose(1, 2).contiguous(), by_index)
+    sample = [0, 1, 63, 257, 400, 511]
+    print("cfg2: oracle on sampled query blocks", flush=True)
+    expected = ora.sparse_attention_mask(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                         mask[:, ::7].numpy(), qblocks_subset=sample)
+    rows = np.concatenate([np.arange(s * 64, s * 64 + 64) for s in sample])
+    _assert_parity(by_index[:, rows], expected[:, rows], what="cfg2 sampled rows")
+
+
+def test_full_size_cfg5_csr_sampled_rows():
+    # BASELINE cfg5 at full size: T=131072 CSR, log-normal density (median 2%).
+    print("cfg5: generating inputs", flush=True)
+    q, k, v = workloads.qkv(0, 131072, 28, 4, 128, torch.bfloat16, use_rope=True,
+                            layout="bthd", device=DEV)
+    indptr, indices = workloads.cfg5_csr(0)
+    ip, ix = indptr.to(DEV), indices.to(DEV)
+    out = direct_index_sparse_csr(q, k, v, ip, ix, scale=128 ** -0.5, row_order=csr_row_order(ip))
+    out_plain = direct_index_sparse_csr(q, k, v, ip, ix, scale=128 ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_plain)
+    counts = (indptr[1:] - indptr[:-1]).view(4, 2048)
+    heavy = int(torch.argmax(counts.sum(0)))
+    sample = sorted({0, 5, 1024, 2047, heavy})
+    print(f"cfg5: oracle on query blocks {sample}", flush=True)
+    qs = torch.zeros(1, 28, 131072, 128)
+    rows = np.concatenate([np.arange(s * 64, s * 64 + 64) for s in sample])
+    qs[:, :, rows] = q[:, :, rows].float().cpu()
+    expected = ora.sparse_attention_csr(qs.numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(),
+                                        indptr.numpy(), indices.numpy(), qblocks_subset=sample)
+    _assert_parity(out[:, rows], expected[:, rows], what="cfg5 sampled rows")
