@@ -1,0 +1,223 @@
+"""Sparse-prefill benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--csr128k/--no-csr128k]
+
+One step = one block-sparse causal GQA prefill of a Qwen2-7B-shaped attention
+layer (BASELINE cfg2: T=32768, 28 query / 4 KV heads, d=128, bf16 Q/K/V ~
+N(0,1) with RoPE theta=1e6, block mask of sink + local-4 + stable top-k at
+~10% causal density), launched through the C ABI
+(spruce_sparse_prefill_mask) with inputs already resident in HBM.
+
+Printed: one JSON line with the BASELINE metric (effective TFLOP/s over the
+computed blocks, 4*64*64*128 FLOP per (query head, selected block)), ms per
+step, the live roofline of the kernel (HIP events on the launch stream) and a
+CPU baseline (the float32 numpy oracle on a bounded sample of the same
+workload).  The 128K direct-index CSR configuration (BASELINE cfg5) is timed
+the same way and reported under "configs".
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "spruce-research_amd"), ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+BLOCK_FLOPS = 4.0 * 64 * 64 * 128  # per (query head, selected 64-key block), d=128
+
+
+def _time_launches(fn, steps, warmup):
+    """Run fn warmup times, then time `steps` launches.
+
+    Returns (wall ms per step bracketed by synchronize, list of per-launch
+    kernel ms from HIP events recorded on the launch stream)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s, e in events:
+        s.record(stream)
+        fn()
+        e.record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    return wall_ms, [s.elapsed_time(e) for s, e in events]
+
+
+def _traffic(name):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(name)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(q, k, v, mask_kv, sample_blocks):
+    """Time the float32 numpy oracle on a sample of query blocks of cfg2."""
+    import numpy as np
+
+    import oracle.attention as ora
+    threads = None
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max((i.get("num_threads") or 0) for i in threadpool_info()) or None
+    except Exception:
+        pass
+    qn, kn, vn = (x.float().cpu().numpy() for x in (q, k, v))
+    mk = mask_kv.cpu().numpy()
+    ora.sparse_attention_mask(qn, kn, vn, mk, qblocks_subset=sample_blocks[:1])  # warm-up
+    t0 = time.perf_counter()
+    ora.sparse_attention_mask(qn, kn, vn, mk, qblocks_subset=sample_blocks)
+    dt = time.perf_counter() - t0
+    G = q.shape[1] // k.shape[1]
+    sel = sum(int(mk[0, g, s, : s + 1].sum()) for g in range(mk.shape[1]) for s in sample_blocks)
+    flops = sel * G * BLOCK_FLOPS
+    return {
+        "value": round(flops / dt / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": threads or os.cpu_count(),
+        "kind": "port",
+        "seconds": round(dt, 3),
+        "sample": (f"oracle/attention.py float32 numpy, {len(sample_blocks)} of 512 query blocks "
+                   f"x 4 KV heads x 7 query heads of cfg2, {sel * G} head-blocks"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-csr128k", action="store_true", help="skip the 128K CSR configuration")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="after timing, run one plain 512 MiB device copy (PMC byte calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU's share of the layer; multi-GPU runs are not part of "
+              "this build (the layer shards by KV head with no exchange, see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from kernels.block_mask import block_sparse_prefill
+    from kernels.direct_index import csr_row_order, direct_index_sparse_csr
+    from spruce_hip import workloads
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+
+    # ---- cfg2: Qwen2-7B layer, T=32768, block mask at ~10% density
+    T, Hq, Hkv, D = 32768, 28, 4, 128
+    q, k, v = workloads.qkv(args.seed, T, Hq, Hkv, D, torch.bfloat16, use_rope=True,
+                            layout="bthd", device="cuda")
+    mask, density = workloads.cfg2_mask(args.seed)
+    mask_d = mask.to(dev)
+    selected = int(mask[:, ::Hq // Hkv].sum())
+    flops = selected * (Hq // Hkv) * BLOCK_FLOPS
+    scale = D ** -0.5
+    fn = lambda: block_sparse_prefill(q, k, v, mask_d, scale)  # noqa: E731
+    wall_ms, kern_ms = _time_launches(fn, args.steps, args.warmup)
+    kmean = statistics.fmean(kern_ms)
+    kmed = statistics.median(kern_ms)
+    achieved = flops / (kmean * 1e-3) / 1e12
+
+    configs = {
+        "cfg2_32k_block_mask": {
+            "ms_median": round(kmed, 4), "ms_min": round(min(kern_ms), 4),
+            "ms_max": round(max(kern_ms), 4),
+            "tflops": round(flops / (kmed * 1e-3) / 1e12, 2),
+            "frac_bf16_peak": round(flops / (kmed * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "density": round(density, 5), "selected_kv_blocks": selected, "flop": flops,
+        }
+    }
+
+    # ---- cfg5: T=131072 direct-index CSR with log-normal row densities
+    if not args.no_csr128k:
+        T5 = 131072
+        q5, k5, v5 = workloads.qkv(args.seed, T5, Hq, Hkv, D, torch.bfloat16, use_rope=True,
+                                   layout="bthd", device="cuda")
+        indptr, indices = workloads.cfg5_csr(args.seed)
+        ip, ix = indptr.to(dev), indices.to(dev)
+        order = csr_row_order(ip)
+        nnz = int(indices.numel())
+        flops5 = nnz * (Hq // Hkv) * BLOCK_FLOPS
+        fn5 = lambda: direct_index_sparse_csr(q5, k5, v5, ip, ix, scale, row_order=order)  # noqa: E731
+        _, k5ms = _time_launches(fn5, max(5, args.steps // 5), max(2, args.warmup // 5))
+        m5 = statistics.median(k5ms)
+        counts = (indptr[1:] - indptr[:-1]).float()
+        configs["cfg5_128k_csr"] = {
+            "ms_median": round(m5, 4), "ms_min": round(min(k5ms), 4), "ms_max": round(max(k5ms), 4),
+            "tflops": round(flops5 / (m5 * 1e-3) / 1e12, 2),
+            "frac_bf16_peak": round(flops5 / (m5 * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "nnz_kv_blocks": nnz, "flop": flops5,
+            "row_blocks_mean": round(float(counts.mean()), 2), "row_blocks_max": int(counts.max()),
+        }
+        del q5, k5, v5
+
+    if args.calib_copy:
+        # A plain copy of known size: reads and writes exactly 512 MiB.  Its
+        # FETCH_SIZE / WRITE_SIZE readings calibrate the PMC byte counters.
+        src = torch.empty(256 * 1024 * 1024, dtype=torch.bfloat16, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    cpu = None
+    if not args.no_cpu:
+        sample = list(range(512))
+        cpu = cpu_baseline(q, k, v, mask[:, ::Hq // Hkv], sample)
+
+    result = {
+        "metric": "sparse-prefill attn ms + effective TFLOP/s, Qwen2-7B layer @32K/128K, 1 GPU",
+        "value": round(flops / (wall_ms * 1e-3) / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) Q/K/V with RoPE, generated on the GPU; seeded block mask)",
+        "config": {
+            "workload": "cfg2: Qwen2-7B attention layer, block-sparse causal GQA prefill, block mask",
+            "seq_len": T, "query_heads": Hq, "kv_heads": Hkv, "head_dim": D, "block": 64,
+            "density": round(density, 5), "batch": 1, "parallelism": "none (1 GPU)",
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": _traffic("cfg2_32k_block_mask"),
+            "kernel": "sparse_prefill_kernel<128, 7, InBF16, false, kModeMask>",
+            "kernel_ms_mean": round(kmean, 4),
+        },
+        "cpu_baseline": cpu,
+        "configs": configs,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()
