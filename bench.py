@@ -154,7 +154,7 @@ def main():
                                    layout="bthd", device="cuda")
         indptr, indices = workloads.cfg5_csr(args.seed)
         ip, ix = indptr.to(dev), indices.to(dev)
-        order = csr_row_order(ip)
+        order = csr_row_order(ip, Hkv)
         nnz = int(indices.numel())
         flops5 = nnz * (Hq // Hkv) * BLOCK_FLOPS
         fn5 = lambda: direct_index_sparse_csr(q5, k5, v5, ip, ix, scale, row_order=order)  # noqa: E731

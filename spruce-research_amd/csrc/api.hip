@@ -55,6 +55,10 @@ int prepare_attention(AttnParams& p, const void* q, const int64_t qs[4], const v
   SPRUCE_REQUIRE(reinterpret_cast<uintptr_t>(out) % 8 == 0 && os[0] % 4 == 0 && os[1] % 4 == 0 &&
                      os[2] % 4 == 0,
                  "out must be 8-byte aligned with strides that are multiples of 4 elements");
+  // Buffer loads address a 64-token block (32-token tile) with 32-bit offsets.
+  SPRUCE_REQUIRE(qs[2] * eb * 32 < ((int64_t)1 << 30) && os[2] * eb * 32 < ((int64_t)1 << 30) &&
+                     ks[2] * eb * 64 < ((int64_t)1 << 30) && vs[2] * eb * 64 < ((int64_t)1 << 30),
+                 "token strides too large");
   p = AttnParams{};
   p.q = q;
   p.k = k;
@@ -78,7 +82,7 @@ int prepare_attention(AttnParams& p, const void* q, const int64_t qs[4], const v
   p.qmul = scale * log2e;
   shape = choose_shape(variant, p.G);
   p.parts = shape.parts;
-  const int64_t grid = (int64_t)B * Hkv * p.Qb * shape.parts;
+  const int64_t grid = ((int64_t)B * Hkv * p.Qb + 7) / 8 * 8 * shape.parts;
   SPRUCE_REQUIRE(grid < ((int64_t)1 << 31), "grid too large");
   return SPRUCE_OK;
 }

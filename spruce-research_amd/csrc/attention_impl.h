@@ -217,6 +217,58 @@ struct BlockIter<kModeMask> {
 };
 
 // ------------------------------------------------------------------ kernel
+// Buffer descriptors: the block's base is folded into the 48-bit base address
+// and num_records bounds the valid bytes, so every load or store beyond the
+// sequence end (ragged last block) reads zeros or is dropped by the hardware
+// range check -- no per-lane branches, and per-lane offsets stay constant.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+constexpr int kOutOfRange = 0x40000000;  // voffset beyond any num_records used here
+
+template <typename TIn>
+__device__ __forceinline__ raw8_t<TIn> buf_load8(__amdgpu_buffer_rsrc_t r, int voff) {
+  if constexpr (TIn::bytes == 2) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+  } else {
+    F32x8 x;
+    x.a = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+    x.b = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16, 0, 0));
+    return x;
+  }
+}
+
+// Rounds 8 loaded elements to the MFMA type, optionally scaled by `mul` first.
+template <typename TIn, bool F16>
+__device__ __forceinline__ uint4 to_mfma_scaled(const raw8_t<TIn>& r, float mul, bool scaled) {
+  if (!scaled) return raw_to_mfma<TIn, F16>(r);
+  float f[8];
+  if constexpr (TIn::bytes == 2) {
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = unpack1<F16>(w[i] & 0xffffu);
+      f[2 * i + 1] = unpack1<F16>(w[i] >> 16);
+    }
+  } else {
+    f[0] = r.a.x; f[1] = r.a.y; f[2] = r.a.z; f[3] = r.a.w;
+    f[4] = r.b.x; f[5] = r.b.y; f[6] = r.b.z; f[7] = r.b.w;
+  }
+  return uint4{pack2<F16>(f[0] * mul, f[1] * mul), pack2<F16>(f[2] * mul, f[3] * mul),
+               pack2<F16>(f[4] * mul, f[5] * mul), pack2<F16>(f[6] * mul, f[7] * mul)};
+}
+
+__device__ __forceinline__ uint32_t word_of(const uint4& r, int k) {
+  return k == 0 ? r.x : k == 1 ? r.y : k == 2 ? r.z : r.w;
+}
+
+// Softmax reference point: the running max is only raised when a row's max
+// grows by more than this (log2 units), so most blocks skip the O rescale.
+// Exponents stay <= 2^8, far inside fp32/bf16/f16 range; the final O / l is
+// unchanged because O and l share the same reference point.
+constexpr float kRescaleThreshold = 8.0f;
+
 template <int D, int WAVES, typename TIn, bool F16, int MODE>
 __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnParams p) {
   constexpr int NTHR = WAVES * 64;
@@ -225,7 +277,7 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
   constexpr int KTILE = kBlock * KSTR;
   constexpr int VTILE = D * VSTR;
   constexpr int BUF = KTILE + VTILE;
-  constexpr int KROWCH = D / 8;                  // 16-byte chunks per K row
+  constexpr int KROWCH = D / 8;                  // 8-element chunks per K row
   constexpr int KCHUNKS = kBlock * KROWCH;
   constexpr int KCH = (KCHUNKS + NTHR - 1) / NTHR;
   constexpr int VTASKS = (kBlock / 4) * (D / 8);  // 4 keys x 8 dims per task
@@ -239,19 +291,26 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hl = lane >> 5;
 
-  // ---- work item
-  const int roww = blockIdx.x / p.parts;
-  const int part = blockIdx.x - roww * p.parts;
+  // ---- work item.  Workgroups go round-robin to the 8 XCDs (blockIdx % 8);
+  // the parts of one row are given consecutive slots on the same XCD so the
+  // second part finds the row's K/V blocks in that XCD's L2.
+  const int nrows = p.B * p.Hkv * p.Qb;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int chunk = slot / p.parts;
+  const int part = slot - chunk * p.parts;
+  const int roww = chunk * 8 + xcd;
+  if (roww >= nrows) return;  // uniform: before any barrier
   int b, g, qb;
   if (MODE == kModeCsr && p.row_order != nullptr) {
     const int r = __builtin_amdgcn_readfirstlane(p.row_order[roww]);
-    if (r < 0 || r >= p.B * p.Hkv * p.Qb) return;  // uniform: before any barrier
+    if (r < 0 || r >= nrows) return;  // uniform: before any barrier
     qb = r % p.Qb;
     const int bg = r / p.Qb;
     g = bg % p.Hkv;
     b = bg / p.Hkv;
   } else {
-    // Heaviest (last) query blocks first: causal rows grow with qb.
+    // Heaviest (last) query blocks first: causal rows grow with qb.  KV head
+    // varies fastest, so XCD x always serves KV head x % Hkv (Hkv | 8).
     const int bh = p.B * p.Hkv;
     qb = p.Qb - 1 - roww / bh;
     const int bg = roww - (roww / bh) * bh;
@@ -262,46 +321,61 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
   const bool active = tile < 2 * p.G;
   const int hq = active ? (tile >> 1) : 0;
   const int head = g * p.G + hq;
-  const int qin = (tile & 1) * 32 + l32;  // query row inside the 64-row block
-  const int qtok = qb * kBlock + qin;
+  const int q0 = qb * kBlock + (tile & 1) * 32;  // first query of this wave's tile
+  const int qin = (tile & 1) * 32 + l32;         // this lane's query row in the block
 
   // ---- Q fragment (B operand of S^T = K Q^T), resident for the whole row
   uint4 qf[KS];
   {
-    const char* qrow = static_cast<const char*>(p.q) +
-        ((int64_t)b * p.qs[0] + (int64_t)head * p.qs[1] + (int64_t)qtok * p.qs[2]) * EB;
-    const bool qv = active && qtok < p.T;
+    const int64_t qrs = p.qs[2] * EB;
+    int nq = p.T - q0;
+    nq = nq < 0 ? 0 : (nq > 32 ? 32 : nq);
+    if (!active) nq = 0;
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(
+        static_cast<const char*>(p.q) + ((int64_t)b * p.qs[0] + (int64_t)head * p.qs[1] + (int64_t)q0 * p.qs[2]) * EB,
+        (uint32_t)(nq * qrs));
+    const int vq = l32 * (int)qrs + 8 * hl * EB;
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk)
-      qf[kk] = load8<TIn, F16>(qrow + (int64_t)(16 * kk + 8 * hl) * EB, qv, p.qmul, p.prescale != 0);
+      qf[kk] = to_mfma_scaled<TIn, F16>(buf_load8<TIn>(rq, vq + 16 * kk * EB), p.qmul, p.prescale != 0);
   }
 
+  // ---- per-lane staging offsets, constant across blocks
   const char* kbase = static_cast<const char*>(p.k) + ((int64_t)b * p.ks[0] + (int64_t)g * p.ks[1]) * EB;
   const char* vbase = static_cast<const char*>(p.v) + ((int64_t)b * p.vs[0] + (int64_t)g * p.vs[1]) * EB;
+  const int krs = (int)(p.ks[2] * EB), vrs = (int)(p.vs[2] * EB);
+  int koff[KCH], klds[KCH];
+#pragma unroll
+  for (int i = 0; i < KCH; ++i) {
+    const int c = tid + i * NTHR;
+    const int key = c / KROWCH, dc = c % KROWCH;
+    koff[i] = c < KCHUNKS ? key * krs + dc * 8 * EB : kOutOfRange;
+    klds[i] = key * KSTR + dc * 8;
+  }
+  int voff[VTK], vlds[VTK];
+#pragma unroll
+  for (int i = 0; i < VTK; ++i) {
+    const int t = tid + i * NTHR;
+    const int a = t & 15, bd = t >> 4;
+    voff[i] = t < VTASKS ? 4 * a * vrs + bd * 8 * EB : kOutOfRange;
+    vlds[i] = 8 * bd * VSTR + vt_pos(4 * a);
+  }
 
   raw8_t<TIn> kst[KCH];
   raw8_t<TIn> vst[VTK][4];
 
   auto load_block = [&](int blk) {
     const int t0 = blk * kBlock;
+    int nk = p.T - t0;
+    nk = nk > kBlock ? kBlock : nk;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + (int64_t)t0 * krs, (uint32_t)(nk * krs));
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + (int64_t)t0 * vrs, (uint32_t)(nk * vrs));
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int c = tid + i * NTHR;
-      const int key = c / KROWCH, dc = c - (c / KROWCH) * KROWCH;
-      const bool ok = (c < KCHUNKS) && (t0 + key < p.T);
-      kst[i] = raw_load8<TIn>(kbase + ((int64_t)(t0 + key) * p.ks[2] + dc * 8) * EB, ok);
-    }
+    for (int i = 0; i < KCH; ++i) kst[i] = buf_load8<TIn>(rk, koff[i]);
 #pragma unroll
-    for (int i = 0; i < VTK; ++i) {
-      const int t = tid + i * NTHR;
-      const int a = t & 15, bd = t >> 4;
+    for (int i = 0; i < VTK; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int key = 4 * a + j;
-        const bool ok = (t < VTASKS) && (t0 + key < p.T);
-        vst[i][j] = raw_load8<TIn>(vbase + ((int64_t)(t0 + key) * p.vs[2] + bd * 8) * EB, ok);
-      }
-    }
+      for (int j = 0; j < 4; ++j) vst[i][j] = buf_load8<TIn>(rv, voff[i] + j * vrs);
   };
 
   auto store_block = [&](int buf) {
@@ -309,33 +383,29 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     uint16_t* Vt = Ks + KTILE;
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
-      const int c = tid + i * NTHR;
-      if (c < KCHUNKS) {
-        const int key = c / KROWCH, dc = c - (c / KROWCH) * KROWCH;
-        *reinterpret_cast<uint4*>(Ks + key * KSTR + dc * 8) = raw_to_mfma<TIn, F16>(kst[i]);
-      }
+      if ((KCHUNKS % NTHR) == 0 || tid + i * NTHR < KCHUNKS)
+        *reinterpret_cast<uint4*>(Ks + klds[i]) = raw_to_mfma<TIn, F16>(kst[i]);
     }
 #pragma unroll
     for (int i = 0; i < VTK; ++i) {
-      const int t = tid + i * NTHR;
-      if (t < VTASKS) {
-        const int a = t & 15, bd = t >> 4;
+      if ((VTASKS % NTHR) == 0 || tid + i * NTHR < VTASKS) {
         const uint4 r0 = raw_to_mfma<TIn, F16>(vst[i][0]);
         const uint4 r1 = raw_to_mfma<TIn, F16>(vst[i][1]);
         const uint4 r2 = raw_to_mfma<TIn, F16>(vst[i][2]);
         const uint4 r3 = raw_to_mfma<TIn, F16>(vst[i][3]);
-        const int pos = vt_pos(4 * a);
+        // Dim e of the four keys -> one 8-byte V^T row segment (v_perm_b32 x2).
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const uint32_t w0 = elem16(r0, e) | (elem16(r1, e) << 16);
-          const uint32_t w1 = elem16(r2, e) | (elem16(r3, e) << 16);
-          *reinterpret_cast<uint2*>(Vt + (8 * bd + e) * VSTR + pos) = uint2{w0, w1};
+          const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+          const uint32_t w0 = __builtin_amdgcn_perm(word_of(r1, e >> 1), word_of(r0, e >> 1), sel);
+          const uint32_t w1 = __builtin_amdgcn_perm(word_of(r3, e >> 1), word_of(r2, e >> 1), sel);
+          *reinterpret_cast<uint2*>(Vt + vlds[i] + e * VSTR) = uint2{w0, w1};
         }
       }
     }
   };
 
-  float m_run = -INFINITY;  // running max of scaled scores (log2 domain)
+  float m_use = -INFINITY;  // softmax reference point (scaled, log2 domain)
   float l_run = 0.f;        // running sum over this lane half's keys
   f32x16_t acc[DT];
 #pragma unroll
@@ -344,63 +414,84 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
   auto compute = [&](int buf, bool diag) {
     const uint16_t* Ks = smem + buf * BUF;
     const uint16_t* Vt = Ks + KTILE;
-    f32x16_t s[2] = {f32x16_t{}, f32x16_t{}};
+    // S^T (64 keys x 32 queries) as two 32x32 tiles, LDS reads one k-step ahead.
+    f32x16_t s0 = f32x16_t{}, s1 = f32x16_t{};
+    const uint16_t* kp = Ks + l32 * KSTR + 8 * hl;
+    uint4 a0 = *reinterpret_cast<const uint4*>(kp);
+    uint4 a1 = *reinterpret_cast<const uint4*>(kp + 32 * KSTR);
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
-      const uint4 a0 = *reinterpret_cast<const uint4*>(Ks + l32 * KSTR + 16 * kk + 8 * hl);
-      const uint4 a1 = *reinterpret_cast<const uint4*>(Ks + (32 + l32) * KSTR + 16 * kk + 8 * hl);
-      s[0] = mfma32x32x16<F16>(a0, qf[kk], s[0]);
-      s[1] = mfma32x32x16<F16>(a1, qf[kk], s[1]);
+      uint4 n0 = a0, n1 = a1;
+      if (kk + 1 < KS) {
+        n0 = *reinterpret_cast<const uint4*>(kp + 16 * (kk + 1));
+        n1 = *reinterpret_cast<const uint4*>(kp + 32 * KSTR + 16 * (kk + 1));
+      }
+      s0 = mfma32x32x16<F16>(a0, qf[kk], s0);
+      s1 = mfma32x32x16<F16>(a1, qf[kk], s1);
+      a0 = n0;
+      a1 = n1;
     }
     if (diag) {
-      // Accumulator register r of key tile c holds key 32c + 8(r/4) + 4(lane/32) + r%4.
+      // Register r of key tile c holds key 32c + 8(r/4) + 4(lane/32) + r%4.
+      const int thr = qin - 4 * hl;
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = 32 * c + 8 * (r >> 2) + 4 * hl + (r & 3);
-          if (key > qin) s[c][r] = -INFINITY;
-        }
+      for (int r = 0; r < 16; ++r) {
+        const int kr = 8 * (r >> 2) + (r & 3);
+        if (kr > thr) s0[r] = -INFINITY;
+        if (32 + kr > thr) s1[r] = -INFINITY;
+      }
     }
-    float mx = -INFINITY;
+    float mx = fmaxf(s0[0], s0[1]);
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
+    for (int r = 2; r < 16; ++r) mx = fmaxf(mx, s0[r]);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[c][r]);
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s1[r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx * p.cs);
-    const float alpha = fast_exp2(m_run - m_new);
-    m_run = m_new;
+    const float cand = mx * p.cs;
+    if (__ballot(cand > m_use + kRescaleThreshold) != 0) {
+      const float m_new = fmaxf(m_use, cand);
+      const float alpha = fast_exp2(m_use - m_new);
+      m_use = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
+    }
+    const float nm = -m_use;
     float psum = 0.f;
     uint4 pk[2][2];
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
+    for (int h2 = 0; h2 < 2; ++h2) {
+      uint32_t w0[4], w1[4];
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        uint32_t w[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float x0 = fast_exp2(fmaf(s[c][8 * h2 + 2 * e], p.cs, -m_new));
-          const float x1 = fast_exp2(fmaf(s[c][8 * h2 + 2 * e + 1], p.cs, -m_new));
-          psum += x0 + x1;
-          w[e] = pack2<F16>(x0, x1);
-        }
-        pk[c][h2] = uint4{w[0], w[1], w[2], w[3]};
+      for (int e = 0; e < 4; ++e) {
+        const float x0 = fast_exp2(fmaf(s0[8 * h2 + 2 * e], p.cs, nm));
+        const float x1 = fast_exp2(fmaf(s0[8 * h2 + 2 * e + 1], p.cs, nm));
+        const float y0 = fast_exp2(fmaf(s1[8 * h2 + 2 * e], p.cs, nm));
+        const float y1 = fast_exp2(fmaf(s1[8 * h2 + 2 * e + 1], p.cs, nm));
+        psum += (x0 + x1) + (y0 + y1);
+        w0[e] = pack2<F16>(x0, x1);
+        w1[e] = pack2<F16>(y0, y1);
       }
-    l_run = l_run * alpha + psum;
+      pk[0][h2] = uint4{w0[0], w0[1], w0[2], w0[3]};
+      pk[1][h2] = uint4{w1[0], w1[1], w1[2], w1[3]};
+    }
+    l_run += psum;
+    // O^T += V^T P^T, V^T fragments one step ahead.
+    const uint16_t* vp = Vt + l32 * VSTR + 8 * hl;
+    uint4 va = *reinterpret_cast<const uint4*>(vp);
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-          const uint4 a = *reinterpret_cast<const uint4*>(Vt + (dt * 32 + l32) * VSTR + 32 * c + 16 * h2 + 8 * hl);
-          acc[dt] = mfma32x32x16<F16>(a, pk[c][h2], acc[dt]);
-        }
+    for (int i = 0; i < DT * 4; ++i) {
+      const int dt = i >> 2, c = (i >> 1) & 1, h2 = i & 1;
+      uint4 vn = va;
+      if (i + 1 < DT * 4) {
+        const int dn = (i + 1) >> 2, cn = ((i + 1) >> 1) & 1, hn = (i + 1) & 1;
+        vn = *reinterpret_cast<const uint4*>(vp + dn * 32 * VSTR + 32 * cn + 16 * hn);
+      }
+      acc[dt] = mfma32x32x16<F16>(va, pk[c][h2], acc[dt]);
+      va = vn;
+    }
   };
 
   BlockIter<MODE> it;
@@ -430,9 +521,13 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
   if (!active) return;
   const float lt = l_run + __shfl_xor(l_run, 32);
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
-  if (qtok >= p.T) return;
-  char* orow = static_cast<char*>(p.o) +
-      ((int64_t)b * p.os[0] + (int64_t)head * p.os[1] + (int64_t)qtok * p.os[2]) * EB;
+  const int64_t ors = p.os[2] * EB;
+  int nq = p.T - q0;
+  nq = nq < 0 ? 0 : (nq > 32 ? 32 : nq);
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(
+      static_cast<char*>(p.o) + ((int64_t)b * p.os[0] + (int64_t)head * p.os[1] + (int64_t)q0 * p.os[2]) * EB,
+      (uint32_t)(nq * ors));
+  const int vo = l32 * (int)ors;
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -441,9 +536,13 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
       const float o0 = acc[dt][4 * j] * inv, o1 = acc[dt][4 * j + 1] * inv;
       const float o2 = acc[dt][4 * j + 2] * inv, o3 = acc[dt][4 * j + 3] * inv;
       if constexpr (EB == 2) {
-        *reinterpret_cast<uint2*>(orow + (int64_t)d * EB) = uint2{pack2<F16>(o0, o1), pack2<F16>(o2, o3)};
+        const uint32_t w[2] = {pack2<F16>(o0, o1), pack2<F16>(o2, o3)};
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned int, w),
+                                              ro, vo + d * EB, 0, 0);
       } else {
-        *reinterpret_cast<float4*>(orow + (int64_t)d * EB) = float4{o0, o1, o2, o3};
+        const float f[4] = {o0, o1, o2, o3};
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, f),
+                                               ro, vo + d * EB, 0, 0);
       }
     }
 }
@@ -468,7 +567,9 @@ inline LaunchShape choose_shape(int variant, int G) {
 
 template <int D, int WAVES, typename TIn, bool F16, int MODE>
 int launch_attention_t(const AttnParams& p, hipStream_t stream) {
-  const int64_t grid = (int64_t)p.B * p.Hkv * p.Qb * p.parts;
+  // Rows are padded to a multiple of the 8 XCDs; the extra workgroups exit.
+  const int64_t rows8 = ((int64_t)p.B * p.Hkv * p.Qb + 7) / 8 * 8;
+  const int64_t grid = rows8 * p.parts;
   hipLaunchKernelGGL((sparse_prefill_kernel<D, WAVES, TIn, F16, MODE>), dim3((unsigned)grid),
                      dim3(WAVES * 64), 0, stream, p);
   return check_launch("sparse_prefill_kernel");

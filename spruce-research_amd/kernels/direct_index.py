@@ -127,10 +127,22 @@ def direct_index_sparse_csr(q, k, v, indptr, indices, scale, block_size=64,
     return out
 
 
-def csr_row_order(indptr):
-    """Dispatch order heaviest-row-first (longest processing time first)."""
-    counts = indptr[1:] - indptr[:-1]
-    return torch.argsort(counts, descending=True, stable=True).to(torch.int32)
+def csr_row_order(indptr, num_kv_heads, batch=1):
+    """Dispatch order for the CSR kernel: heaviest rows first, heads interleaved.
+
+    Within each (batch, KV head) the query blocks are sorted by row length,
+    longest first (longest processing time first balances the variable
+    lengths).  Position ``i`` of the order holds a row of (batch, KV head)
+    ``i % (batch*num_kv_heads)``; the kernel deals consecutive positions to the
+    8 XCDs, so with ``batch*num_kv_heads`` dividing 8 each XCD's L2 serves one
+    KV head's K/V.
+    """
+    bh = batch * num_kv_heads
+    counts = (indptr[1:] - indptr[:-1]).view(bh, -1)
+    qblocks = counts.shape[1]
+    order = torch.argsort(counts, dim=1, descending=True, stable=True)
+    rows = order + torch.arange(bh, device=indptr.device)[:, None] * qblocks
+    return rows.t().reshape(-1).to(torch.int32).contiguous()
 
 
 def kernel_runtime_metadata(kernel_variant):

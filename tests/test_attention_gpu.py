@@ -167,7 +167,7 @@ def test_csr_rows_with_row_order_and_empty_rows():
     dev = [x.transpose(1, 2).contiguous().to(DEV).transpose(1, 2) for x in (q, k, v)]
     ip, ix = torch.from_numpy(indptr).to(DEV), torch.from_numpy(indices).to(DEV)
     plain = direct_index_sparse_csr(*dev, ip, ix, scale=D ** -0.5)
-    ordered = direct_index_sparse_csr(*dev, ip, ix, scale=D ** -0.5, row_order=csr_row_order(ip))
+    ordered = direct_index_sparse_csr(*dev, ip, ix, scale=D ** -0.5, row_order=csr_row_order(ip, Hkv))
     _assert_parity(plain, expected, what="csr")
     assert torch.equal(plain, ordered)
 
@@ -253,7 +253,7 @@ def test_full_size_cfg5_csr_sampled_rows():
                             layout="bthd", device=DEV)
     indptr, indices = workloads.cfg5_csr(0)
     ip, ix = indptr.to(DEV), indices.to(DEV)
-    out = direct_index_sparse_csr(q, k, v, ip, ix, scale=128 ** -0.5, row_order=csr_row_order(ip))
+    out = direct_index_sparse_csr(q, k, v, ip, ix, scale=128 ** -0.5, row_order=csr_row_order(ip, 4))
     out_plain = direct_index_sparse_csr(q, k, v, ip, ix, scale=128 ** -0.5)
     torch.cuda.synchronize()
     assert torch.equal(out, out_plain)
