@@ -120,6 +120,60 @@ int spruce_sparse_prefill_mask(
     void* out, const int64_t os[4],
     void* stream);
 
+/* ------------------------------------------------------------------------
+ * Selector front end.  These results are reproducible bit for bit: every
+ * float is produced by a fixed sequence of IEEE single-precision operations
+ * (documented in the library source) so the selected block indices can be
+ * compared exactly with a CPU restatement.
+ * ---------------------------------------------------------------------- */
+
+/*
+ * Block pooling of Q and K into per-64-token-block summaries.
+ *   q [B, Hq, T, D] (strides qs) -> q_mean float32 [B, Hkv, ceil(T/64), D]:
+ *     the query heads of each KV group averaged per token, then the block mean
+ *     (replaces _group_avg_tokens + the prototype-0 mean of _proto_pool_seq,
+ *     teacher/chunked_extract.py:75-80 and :27-72; the reference rounds each
+ *     step to the model dtype, this computes in float32).
+ *   k [B, Hkv, T, D] (strides ks) -> k_sum float32 [B, Hkv, ceil(T/64), 2, D]:
+ *     prototype 0 = block mean (the leaf summary of sparse/summaries.py:52-142
+ *     with all tokens valid), prototype 1 = per-dim block max.
+ * Either input may be NULL to skip it.  D % 8 == 0.
+ */
+int spruce_selector_pool(const void* q, const int64_t qs[4], const void* k, const int64_t ks[4],
+                         int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D, int dtype,
+                         float* q_mean, float* k_sum, void* stream);
+
+/*
+ * out[n][j] = sum_d x[n][d] * w[d][j] (float32, sequential fused multiply-add
+ * over d).  x [N, D], w [D, P], out [N, P], all contiguous.
+ * Replaces FlatGate.project_queries / project_keys (selector/gate.py:120-127).
+ */
+int spruce_gate_project(const float* x, const float* w, int64_t N, int64_t D, int64_t P, float* out,
+                        void* stream);
+
+/*
+ * MaxSim block scores: scores[s][i][j] = max over prototype pairs (a, c) of
+ * qp[s][i][a] . kp[s][j][c], divided by div (= sqrt(P)).  With causal != 0
+ * only j <= i is computed and j > i is written as -inf.
+ * qp [S, Qb, Pq, P], kp [S, Kb, Pk, P], scores [S, Qb, Kb] contiguous.
+ * Replaces FlatGate.forward (selector/gate.py:29-101) plus the causal mask of
+ * selector/recall.py:26-35.
+ */
+int spruce_gate_scores(const float* qp, const float* kp, int64_t S, int64_t Qb, int64_t Kb,
+                       int64_t Pq, int64_t Pk, int64_t P, float div, int causal, float* scores,
+                       void* stream);
+
+/*
+ * Causal top-k block selection per row: the k largest of scores[r][i][0..i]
+ * (ties to the lower block index, the stable descending argsort of
+ * selector/baselines.py:59-62), written ascending into out[r][i][0..k) with
+ * -1 padding when the row has fewer than k causal blocks -- the
+ * selected_blocks row layout (interfaces/selected_blocks_spec.md).
+ * scores [R, Qb, Kb] float32, out [R, Qb, k] int32, contiguous; Kb <= 8192.
+ */
+int spruce_causal_topk(const float* scores, int64_t R, int64_t Qb, int64_t Kb, int64_t k, int32_t* out,
+                       void* stream);
+
 /*
  * Launch configuration the attention entry points use for a shape, as JSON:
  * {"variant":..,"best_config":{..}}.  Replaces kernel_runtime_metadata

@@ -1,0 +1,407 @@
+// Selector front end on gfx950: block pooling, gate projection, MaxSim block
+// scores and causal top-k block selection.
+//
+// Selected block indices are compared bit for bit with a CPU restatement, so
+// every floating-point value is produced by a fixed sequence of IEEE single
+// operations (this file is built with -ffp-contract=off; fused multiply-adds
+// appear only where __builtin_fmaf is written, divisions are IEEE):
+//   pool    per token the G query heads are summed left to right; token t of a
+//           64-token block belongs to lane t % L (L = min(64, 256 / (D/8)));
+//           a lane folds its tokens in increasing order starting from the first
+//           token's value; lanes combine by a halving tree; the sum is divided
+//           by G * (real tokens).  Missing tokens add +0.0f to sums, nothing to
+//           maxima.  (teacher/chunked_extract.py:75-80 group average,
+//           :27-72 prototype 0 block mean; plus the per-dim block max.)
+//   project fmaf chain over the input dim, from 0 (selector/gate.py:120-127).
+//   scores  max over prototype pairs (query prototype major, first pair taken
+//           as is, later pairs replace it only when strictly larger) of fmaf
+//           chains over the projection dim, divided by sqrt(p)
+//           (selector/gate.py:29-101); above the diagonal -inf
+//           (selector/recall.py:26-35).
+//   top-k   per row the k largest causal scores, ties to the lower block index
+//           (stable descending argsort, selector/baselines.py:59-62), written
+//           ascending with -1 padding (interfaces/selected_blocks_spec.md).
+//
+// The pooling kernel streams Q and K once from HBM (the dominant cost of the
+// front end: Q is 7x the bytes of K at 28/4 heads); the rest touches only the
+// pooled summaries and the [Qb, Kb] score matrix.
+#include "common.h"
+
+namespace spruce {
+
+constexpr int kSelBlock = 64;
+
+struct PoolParams {
+  const void* q;
+  const void* k;
+  int64_t qs[4], ks[4];
+  int B, Hq, Hkv, T, D, G, nb, dtype;
+  float* q_mean;  // [B, Hkv, nb, D]
+  float* k_sum;   // [B, Hkv, nb, 2, D] (mean, max)
+};
+
+__device__ __forceinline__ void load8f(const void* base, int64_t elem, int dtype, float* out) {
+  if (dtype == SPRUCE_DTYPE_F32) {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + elem);
+    const float4 a = p[0], b = p[1];
+    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+    out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+  } else {
+    const uint4 r = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + elem);
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+    const bool f16 = dtype == SPRUCE_DTYPE_F16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = f16 ? unpack1<true>(w[i] & 0xffffu) : unpack1<false>(w[i] & 0xffffu);
+      out[2 * i + 1] = f16 ? unpack1<true>(w[i] >> 16) : unpack1<false>(w[i] >> 16);
+    }
+  }
+}
+
+// Total order on floats as unsigned keys (+0 above -0).
+__device__ __forceinline__ uint32_t order_key(float f) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float max_total(float a, float b) { return order_key(b) > order_key(a) ? b : a; }
+
+// One workgroup per (batch, KV head, 64-token block); thread = (token lane l,
+// dim chunk c of 8 dims).
+__global__ __launch_bounds__(256) void block_pool_kernel(const PoolParams p) {
+  __shared__ float red[256 * 8];
+  __shared__ float redmax[256 * 8];
+  const int dch = p.D / 8;
+  const int L = (256 / dch) > kSelBlock ? kSelBlock : 256 / dch;
+  const int per = kSelBlock / L;
+  const int tid = threadIdx.x;
+  const int l = tid / dch, c = tid - (tid / dch) * dch;
+  int w = blockIdx.x;
+  const int blk = w % p.nb;
+  w /= p.nb;
+  const int g = w % p.Hkv;
+  const int b = w / p.Hkv;
+  const int t0 = blk * kSelBlock;
+  int n = p.T - t0;
+  n = n > kSelBlock ? kSelBlock : n;
+  const bool work = tid < dch * L;
+
+  if (p.q) {
+    float acc[8];
+    if (work) {
+      for (int i = 0; i < per; ++i) {
+        const int t = t0 + l + i * L;
+        float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (t < p.T) {
+          load8f(p.q, (int64_t)b * p.qs[0] + (int64_t)(g * p.G) * p.qs[1] + (int64_t)t * p.qs[2] + 8 * c, p.dtype, s);
+          for (int h = 1; h < p.G; ++h) {
+            float x[8];
+            load8f(p.q, (int64_t)b * p.qs[0] + (int64_t)(g * p.G + h) * p.qs[1] + (int64_t)t * p.qs[2] + 8 * c,
+                   p.dtype, x);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) s[e] = s[e] + x[e];
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = (i == 0) ? s[e] : acc[e] + s[e];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) red[(l * dch + c) * 8 + e] = acc[e];
+    }
+    __syncthreads();
+    for (int st = L / 2; st >= 1; st /= 2) {
+      if (work && l < st) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          red[(l * dch + c) * 8 + e] = red[(l * dch + c) * 8 + e] + red[((l + st) * dch + c) * 8 + e];
+      }
+      __syncthreads();
+    }
+    if (work && l == 0) {
+      const float den = (float)(p.G * n);
+      float* o = p.q_mean + (((int64_t)b * p.Hkv + g) * p.nb + blk) * p.D + 8 * c;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = red[c * 8 + e] / den;
+    }
+    __syncthreads();
+  }
+
+  if (p.k) {
+    float acc[8], mx[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mx[e] = -INFINITY;
+    if (work) {
+      for (int i = 0; i < per; ++i) {
+        const int t = t0 + l + i * L;
+        float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (t < p.T) {
+          load8f(p.k, (int64_t)b * p.ks[0] + (int64_t)g * p.ks[1] + (int64_t)t * p.ks[2] + 8 * c, p.dtype, s);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) mx[e] = max_total(mx[e], s[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = (i == 0) ? s[e] : acc[e] + s[e];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        red[(l * dch + c) * 8 + e] = acc[e];
+        redmax[(l * dch + c) * 8 + e] = mx[e];
+      }
+    }
+    __syncthreads();
+    for (int st = L / 2; st >= 1; st /= 2) {
+      if (work && l < st) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          red[(l * dch + c) * 8 + e] = red[(l * dch + c) * 8 + e] + red[((l + st) * dch + c) * 8 + e];
+          redmax[(l * dch + c) * 8 + e] = max_total(redmax[(l * dch + c) * 8 + e], redmax[((l + st) * dch + c) * 8 + e]);
+        }
+      }
+      __syncthreads();
+    }
+    if (work && l == 0) {
+      const float den = (float)n;
+      float* o = p.k_sum + ((((int64_t)b * p.Hkv + g) * p.nb + blk) * 2) * p.D + 8 * c;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        o[e] = red[c * 8 + e] / den;
+        o[p.D + e] = redmax[c * 8 + e];
+      }
+    }
+  }
+}
+
+// out[n][j] = fmaf chain over d of x[n][d] * w[d][j]; one thread per output.
+__global__ __launch_bounds__(256) void project_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                      int64_t N, int D, int P, float* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= N * P) return;
+  const int64_t n = idx / P;
+  const int j = (int)(idx - n * P);
+  const float* xr = x + n * D;
+  float acc = 0.f;
+  for (int d = 0; d < D; ++d) acc = __builtin_fmaf(xr[d], w[(int64_t)d * P + j], acc);
+  out[idx] = acc;
+}
+
+// MaxSim scores over a tile of 16 query blocks x 64 key blocks.
+constexpr int kTI = 16, kTJ = 64;
+struct ScoreParams {
+  const float* qp;  // [BG, Qb, Pq, P]
+  const float* kp;  // [BG, Kb, Pk, P]
+  float* scores;    // [BG, Qb, Kb]
+  int Qb, Kb, Pq, Pk, P;
+  float div;
+  int causal;  // 1: j > i is -inf and not computed
+};
+
+__global__ __launch_bounds__(256) void gate_scores_kernel(const ScoreParams p) {
+  extern __shared__ float lds[];
+  const int bg = blockIdx.z;
+  const int i0 = blockIdx.x * kTI, j0 = blockIdx.y * kTJ;
+  const int tid = threadIdx.x;
+  const int jl = tid & 63, ig = tid >> 6;
+  const int krow = p.Pk * p.P + 4;  // padded key row (floats), keeps lanes on distinct banks
+  const int j = j0 + jl;
+  float* out = p.scores + (int64_t)bg * p.Qb * p.Kb;
+  if (p.causal && j0 > i0 + kTI - 1) {
+    // Entirely above the diagonal.
+    for (int r = 0; r < 4; ++r) {
+      const int i = i0 + ig * 4 + r;
+      if (i < p.Qb && j < p.Kb) out[(int64_t)i * p.Kb + j] = -INFINITY;
+    }
+    return;
+  }
+  float* qs = lds;                          // [kTI][Pq*P]
+  float* ks = lds + kTI * p.Pq * p.P;       // [kTJ][krow]
+  const int qrow = p.Pq * p.P;
+  for (int e = tid; e < kTI * qrow; e += 256) {
+    const int r = e / qrow, off = e - r * qrow;
+    const int i = i0 + r;
+    qs[e] = i < p.Qb ? p.qp[((int64_t)bg * p.Qb + i) * qrow + off] : 0.f;
+  }
+  const int kr = p.Pk * p.P;
+  for (int e = tid; e < kTJ * kr; e += 256) {
+    const int r = e / kr, off = e - r * kr;
+    const int jj = j0 + r;
+    ks[r * krow + off] = jj < p.Kb ? p.kp[((int64_t)bg * p.Kb + jj) * kr + off] : 0.f;
+  }
+  __syncthreads();
+  float best[4];
+  for (int a = 0; a < p.Pq; ++a)
+    for (int c = 0; c < p.Pk; ++c) {
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      const float* kv = ks + jl * krow + c * p.P;
+      for (int e = 0; e < p.P; e += 4) {
+        const float4 y = *reinterpret_cast<const float4*>(kv + e);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float4 x = *reinterpret_cast<const float4*>(qs + (ig * 4 + r) * qrow + a * p.P + e);
+          acc[r] = __builtin_fmaf(x.x, y.x, acc[r]);
+          acc[r] = __builtin_fmaf(x.y, y.y, acc[r]);
+          acc[r] = __builtin_fmaf(x.z, y.z, acc[r]);
+          acc[r] = __builtin_fmaf(x.w, y.w, acc[r]);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) best[r] = (a == 0 && c == 0) ? acc[r] : (acc[r] > best[r] ? acc[r] : best[r]);
+    }
+  for (int r = 0; r < 4; ++r) {
+    const int i = i0 + ig * 4 + r;
+    if (i < p.Qb && j < p.Kb) out[(int64_t)i * p.Kb + j] = (!p.causal || j <= i) ? best[r] / p.div : -INFINITY;
+  }
+}
+
+// Causal top-k per row: radix select (4 passes of 8 bits over order keys) for
+// the k-th largest key, then an in-order compaction that takes every larger key
+// and the lowest-index entries equal to it.  One workgroup per row.
+constexpr int kTopkMaxKb = 8192;
+__global__ __launch_bounds__(256) void causal_topk_kernel(const float* __restrict__ scores, int Qb, int Kb, int k,
+                                                          int32_t* __restrict__ out) {
+  __shared__ uint32_t keys[kTopkMaxKb];
+  __shared__ int hist[256];
+  __shared__ int sel_bin, sel_rem;
+  const int row = blockIdx.x;  // r * Qb + i
+  const int i = row % Qb;
+  const int tid = threadIdx.x;
+  const int n = i + 1 < Kb ? i + 1 : Kb;
+  int32_t* o = out + (int64_t)row * k;
+  if (n <= k) {
+    for (int t = tid; t < k; t += 256) o[t] = t < n ? t : -1;
+    return;
+  }
+  const float* srow = scores + (int64_t)row * Kb;
+  for (int j = tid; j < n; j += 256) keys[j] = order_key(srow[j] + 0.0f);  // -0 -> +0
+  uint32_t prefix = 0, mask = 0;
+  int rem = k;
+  for (int pass = 3; pass >= 0; --pass) {
+    hist[tid] = 0;
+    __syncthreads();
+    const int sh = 8 * pass;
+    for (int j = tid; j < n; j += 256)
+      if ((keys[j] & mask) == prefix) atomicAdd(&hist[(keys[j] >> sh) & 255], 1);
+    __syncthreads();
+    if (tid == 0) {
+      int cum = 0, bin = 0;
+      for (int bb = 255; bb >= 0; --bb) {
+        if (cum + hist[bb] >= rem) {
+          bin = bb;
+          break;
+        }
+        cum += hist[bb];
+      }
+      sel_bin = bin;
+      sel_rem = rem - cum;
+    }
+    __syncthreads();
+    prefix |= (uint32_t)sel_bin << sh;
+    mask |= 255u << sh;
+    rem = sel_rem;
+    __syncthreads();
+  }
+  // prefix = key of the k-th largest; take `rem` of the entries equal to it.
+  if (tid < 64) {
+    const uint32_t thr = prefix;
+    int eq_base = 0, out_base = 0;
+    const uint64_t lt = (tid == 0) ? 0ull : (~0ull >> (64 - tid));
+    for (int c0 = 0; c0 < n; c0 += 64) {
+      const int j = c0 + tid;
+      const uint32_t key = j < n ? keys[j] : 0u;
+      const bool eq = j < n && key == thr;
+      const uint64_t eqb = __ballot(eq);
+      const int rank = eq_base + __popcll(eqb & lt);
+      const bool sel = j < n && (key > thr || (eq && rank < rem));
+      const uint64_t sb = __ballot(sel);
+      if (sel) o[out_base + __popcll(sb & lt)] = j;
+      eq_base += __popcll(eqb);
+      out_base += __popcll(sb);
+    }
+  }
+}
+
+}  // namespace spruce
+
+using namespace spruce;
+
+extern "C" int spruce_selector_pool(const void* q, const int64_t qs[4], const void* k, const int64_t ks[4],
+                                    int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D, int dtype,
+                                    float* q_mean, float* k_sum, void* stream) {
+  SPRUCE_REQUIRE(q || k, "nothing to pool: q and k are both NULL");
+  SPRUCE_REQUIRE(B >= 1 && T >= 1 && Hkv >= 1 && Hq >= Hkv && Hq % Hkv == 0, "invalid shape");
+  SPRUCE_REQUIRE(D >= 8 && D <= 2048 && D % 8 == 0, "head_dim must be a multiple of 8 (<= 2048), got %lld",
+                 (long long)D);
+  SPRUCE_REQUIRE(dtype == SPRUCE_DTYPE_BF16 || dtype == SPRUCE_DTYPE_F16 || dtype == SPRUCE_DTYPE_F32,
+                 "unsupported dtype code %d", dtype);
+  SPRUCE_REQUIRE(!q || (qs && qs[3] == 1 && q_mean), "q needs strides with a contiguous last dim and q_mean");
+  SPRUCE_REQUIRE(!k || (ks && ks[3] == 1 && k_sum), "k needs strides with a contiguous last dim and k_sum");
+  const int per16 = dtype == SPRUCE_DTYPE_F32 ? 4 : 8;
+  if (q) SPRUCE_REQUIRE(reinterpret_cast<uintptr_t>(q) % 16 == 0 && qs[0] % per16 == 0 && qs[1] % per16 == 0 &&
+                            qs[2] % per16 == 0, "q rows must be 16-byte aligned");
+  if (k) SPRUCE_REQUIRE(reinterpret_cast<uintptr_t>(k) % 16 == 0 && ks[0] % per16 == 0 && ks[1] % per16 == 0 &&
+                            ks[2] % per16 == 0, "k rows must be 16-byte aligned");
+  PoolParams p{};
+  p.q = q;
+  p.k = k;
+  for (int i = 0; i < 4; ++i) {
+    p.qs[i] = q ? qs[i] : 0;
+    p.ks[i] = k ? ks[i] : 0;
+  }
+  p.B = (int)B;
+  p.Hq = (int)Hq;
+  p.Hkv = (int)Hkv;
+  p.T = (int)T;
+  p.D = (int)D;
+  p.G = (int)(Hq / Hkv);
+  p.nb = (int)((T + kSelBlock - 1) / kSelBlock);
+  p.dtype = dtype;
+  p.q_mean = q_mean;
+  p.k_sum = k_sum;
+  const int64_t grid = B * Hkv * p.nb;
+  SPRUCE_REQUIRE(grid < ((int64_t)1 << 31), "grid too large");
+  hipLaunchKernelGGL(block_pool_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, p);
+  return check_launch("block_pool_kernel");
+}
+
+extern "C" int spruce_gate_project(const float* x, const float* w, int64_t N, int64_t D, int64_t P, float* out,
+                                   void* stream) {
+  SPRUCE_REQUIRE(x && w && out, "x, w and out must be non-null");
+  SPRUCE_REQUIRE(N >= 1 && D >= 1 && P >= 1 && N * P < ((int64_t)1 << 40), "invalid projection shape");
+  const int64_t blocks = (N * P + 255) / 256;
+  SPRUCE_REQUIRE(blocks < ((int64_t)1 << 31), "projection too large");
+  hipLaunchKernelGGL(project_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, x, w, N, (int)D,
+                     (int)P, out);
+  return check_launch("project_kernel");
+}
+
+extern "C" int spruce_gate_scores(const float* qp, const float* kp, int64_t BG, int64_t Qb, int64_t Kb, int64_t Pq,
+                                  int64_t Pk, int64_t P, float div, int causal, float* scores, void* stream) {
+  SPRUCE_REQUIRE(qp && kp && scores, "qp, kp and scores must be non-null");
+  SPRUCE_REQUIRE(BG >= 1 && Qb >= 1 && Kb >= 1 && Pq >= 1 && Pk >= 1, "invalid score shape");
+  SPRUCE_REQUIRE(P >= 4 && P % 4 == 0, "projection dim must be a positive multiple of 4, got %lld", (long long)P);
+  SPRUCE_REQUIRE(reinterpret_cast<uintptr_t>(qp) % 16 == 0 && reinterpret_cast<uintptr_t>(kp) % 16 == 0,
+                 "qp and kp must be 16-byte aligned");
+  const int64_t lds = (int64_t)(kTI * Pq * P + kTJ * (Pk * P + 4)) * 4;
+  SPRUCE_REQUIRE(lds <= 160 * 1024, "prototype tiles need %lld bytes of LDS (max 163840)", (long long)lds);
+  SPRUCE_REQUIRE(BG < 65536, "too many (batch, head) slabs");
+  ScoreParams p{qp, kp, scores, (int)Qb, (int)Kb, (int)Pq, (int)Pk, (int)P, div, causal ? 1 : 0};
+  const dim3 grid((unsigned)((Qb + kTI - 1) / kTI), (unsigned)((Kb + kTJ - 1) / kTJ), (unsigned)BG);
+  if (lds > 64 * 1024) {
+    const hipError_t e = hipFuncSetAttribute((const void*)gate_scores_kernel,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return set_error((int)e, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+  }
+  hipLaunchKernelGGL(gate_scores_kernel, grid, dim3(256), (size_t)lds, (hipStream_t)stream, p);
+  return check_launch("gate_scores_kernel");
+}
+
+extern "C" int spruce_causal_topk(const float* scores, int64_t R, int64_t Qb, int64_t Kb, int64_t k, int32_t* out,
+                                  void* stream) {
+  SPRUCE_REQUIRE(scores && out, "scores and out must be non-null");
+  SPRUCE_REQUIRE(R >= 1 && Qb >= 1 && Kb >= 1 && k >= 1, "invalid top-k shape");
+  SPRUCE_REQUIRE(Kb <= kTopkMaxKb, "at most %d key blocks per row are supported, got %lld", kTopkMaxKb,
+                 (long long)Kb);
+  SPRUCE_REQUIRE(R * Qb < ((int64_t)1 << 31), "too many rows");
+  hipLaunchKernelGGL(causal_topk_kernel, dim3((unsigned)(R * Qb)), dim3(256), 0, (hipStream_t)stream, scores,
+                     (int)Qb, (int)Kb, (int)k, out);
+  return check_launch("causal_topk_kernel");
+}

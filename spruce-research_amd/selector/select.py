@@ -1,0 +1,150 @@
+"""Flat selector front end on gfx950: pool -> project -> MaxSim score -> causal top-k.
+
+The flat route of the reference's selector (scripts/eval_gate.py:70-72):
+FlatGate scoring (selector/gate.py:29-101) over pooled block features
+(teacher/chunked_extract.py:27-80), the causal mask and top-k of
+selector/recall.py:26-35 with the stable lowest-index tie rule of
+selector/baselines.py:59-62, producing rows in the selected_blocks layout
+(interfaces/selected_blocks_spec.md).  Every step is one HIP kernel behind the
+C ABI; the float results are bit-reproducible (fixed IEEE operation order), so
+the selected indices are exactly those of the CPU restatement.
+
+Shapes follow the reference: query ``[B,Hq,T,D]``, key ``[B,Hkv,T,D]`` (any
+strides with a contiguous last dim), gate weights ``[D, P]`` float32 (one
+layer of FlatGate's ``[L, d, p]``).
+"""
+import math
+
+import torch
+
+import spruce_hip
+
+BLOCK = 64
+
+
+def _cuda(t, name):
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a GPU tensor (HIP selector)")
+
+
+def pool_blocks(query=None, key=None):
+    """Per-64-token-block summaries.
+
+    query ``[B,Hq,T,D]`` -> ``q_mean [B,Hkv,nb,D]`` float32: query heads averaged
+    within each KV group per token, then the block mean (needs ``key`` for Hkv
+    or pass ``num_kv_heads`` via key's shape).  key ``[B,Hkv,T,D]`` ->
+    ``k_sum [B,Hkv,nb,2,D]`` float32: block mean and per-dim block max.
+    """
+    if query is None and key is None:
+        raise ValueError("pool_blocks needs query and/or key")
+    ref = key if key is not None else query
+    _cuda(ref, "key" if key is not None else "query")
+    if key is None:
+        raise ValueError("pool_blocks needs key to know the KV head count")
+    B, Hkv, T, D = key.shape
+    Hq = query.shape[1] if query is not None else Hkv
+    if query is not None:
+        _cuda(query, "query")
+        if query.shape[0] != B or query.shape[2:] != key.shape[2:] or Hq % Hkv:
+            raise ValueError("query must be [B, Hq, T, D] with Hq a multiple of key's KV heads")
+        if query.dtype != key.dtype:
+            raise ValueError("query and key must share a dtype")
+    if D % 8:
+        raise ValueError(f"head_dim must be a multiple of 8, got {D}")
+    nb = (T + BLOCK - 1) // BLOCK
+    q_mean = torch.empty((B, Hkv, nb, D), device=key.device, dtype=torch.float32) if query is not None else None
+    k_sum = torch.empty((B, Hkv, nb, 2, D), device=key.device, dtype=torch.float32)
+    with torch.cuda.device(key.device):
+        rc = spruce_hip.lib().spruce_selector_pool(
+            spruce_hip.ptr(query), spruce_hip.strides(query) if query is not None else None,
+            spruce_hip.ptr(key), spruce_hip.strides(key),
+            B, Hq, Hkv, T, D, spruce_hip.dtype_code(key),
+            spruce_hip.ptr(q_mean), spruce_hip.ptr(k_sum), spruce_hip.stream_of(key))
+    spruce_hip.check(rc, "spruce_selector_pool")
+    return q_mean, k_sum
+
+
+def project(x, W):
+    """``x [..., D] @ W [D, P]`` in float32 with a sequential fused multiply-add over D."""
+    _cuda(x, "x")
+    if x.dtype != torch.float32 or W.dtype != torch.float32:
+        raise ValueError("projection inputs must be float32")
+    if W.dim() != 2 or x.shape[-1] != W.shape[0]:
+        raise ValueError(f"shape mismatch: x {tuple(x.shape)} @ W {tuple(W.shape)}")
+    x2 = x.reshape(-1, x.shape[-1]).contiguous()
+    W = W.to(x.device).contiguous()
+    N, D = x2.shape
+    P = W.shape[1]
+    out = torch.empty((N, P), device=x.device, dtype=torch.float32)
+    with torch.cuda.device(x.device):
+        rc = spruce_hip.lib().spruce_gate_project(
+            spruce_hip.ptr(x2), spruce_hip.ptr(W), N, D, P, spruce_hip.ptr(out), spruce_hip.stream_of(x))
+    spruce_hip.check(rc, "spruce_gate_project")
+    return out.reshape(x.shape[:-1] + (P,))
+
+
+def gate_scores(qp, kp, causal=True, div=None):
+    """MaxSim scores ``[S, Qb, Kb]`` from projected prototypes ``qp [S,Qb,Pq,P]``
+    and ``kp [S,Kb,Pk,P]``, divided by ``div`` (default sqrt(P)); with
+    ``causal`` the entries above the diagonal are -inf."""
+    _cuda(qp, "qp")
+    if qp.dim() != 4 or kp.dim() != 4 or qp.shape[0] != kp.shape[0] or qp.shape[3] != kp.shape[3]:
+        raise ValueError("qp must be [S,Qb,Pq,P] and kp [S,Kb,Pk,P]")
+    if qp.dtype != torch.float32 or kp.dtype != torch.float32:
+        raise ValueError("projected prototypes must be float32")
+    qp = qp.contiguous()
+    kp = kp.contiguous()
+    S, Qb, Pq, P = qp.shape
+    Kb, Pk = kp.shape[1], kp.shape[2]
+    d = math.sqrt(P) if div is None else float(div)
+    out = torch.empty((S, Qb, Kb), device=qp.device, dtype=torch.float32)
+    with torch.cuda.device(qp.device):
+        rc = spruce_hip.lib().spruce_gate_scores(
+            spruce_hip.ptr(qp), spruce_hip.ptr(kp), S, Qb, Kb, Pq, Pk, P, d, int(bool(causal)),
+            spruce_hip.ptr(out), spruce_hip.stream_of(qp))
+    spruce_hip.check(rc, "spruce_gate_scores")
+    return out
+
+
+def causal_topk_blocks(scores, k):
+    """Row-wise causal top-k of ``scores [..., Qb, Kb]`` -> int32 ``[..., Qb, k]``
+    ascending with -1 padding; ties go to the lower block index."""
+    _cuda(scores, "scores")
+    if scores.dtype != torch.float32:
+        raise ValueError("scores must be float32")
+    if k < 1:
+        raise ValueError(f"k must be >= 1, got {k}")
+    Qb, Kb = scores.shape[-2:]
+    s = scores.reshape(-1, Qb, Kb).contiguous()
+    R = s.shape[0]
+    out = torch.empty((R, Qb, k), device=scores.device, dtype=torch.int32)
+    with torch.cuda.device(scores.device):
+        rc = spruce_hip.lib().spruce_causal_topk(
+            spruce_hip.ptr(s), R, Qb, Kb, k, spruce_hip.ptr(out), spruce_hip.stream_of(scores))
+    spruce_hip.check(rc, "spruce_causal_topk")
+    return out.reshape(scores.shape[:-1] + (k,))
+
+
+def select_blocks(query, key, Wq, Wk, top_k=32, return_intermediates=False):
+    """The flat selector over one layer.
+
+    Pools Q (group mean, block mean) and K (block mean and max), projects them
+    with ``Wq``/``Wk`` (``[D, P]`` float32), scores every causal (query block,
+    key block) pair by MaxSim over the key summaries {mean, max}, and keeps the
+    top ``top_k`` blocks per (KV head, query block).
+
+    Returns ``selected`` int32 ``[B, 1, Hkv, nb, top_k]`` (the selected_blocks
+    layout with one layer), or a dict with every intermediate when
+    ``return_intermediates``.
+    """
+    q_mean, k_sum = pool_blocks(query, key)
+    B, Hkv, nb, D = q_mean.shape
+    qp = project(q_mean, Wq)                       # [B,Hkv,nb,P]
+    kp = project(k_sum, Wk)                        # [B,Hkv,nb,2,P]
+    P = qp.shape[-1]
+    sc = gate_scores(qp.reshape(B * Hkv, nb, 1, P), kp.reshape(B * Hkv, nb, 2, P), causal=True)
+    sel = causal_topk_blocks(sc, top_k).reshape(B, Hkv, nb, top_k)[:, None]
+    if not return_intermediates:
+        return sel
+    return {"q_mean": q_mean, "k_sum": k_sum, "qp": qp, "kp": kp,
+            "scores": sc.reshape(B, Hkv, nb, nb), "selected": sel}

@@ -148,3 +148,22 @@ def cfg5_csr(seed=0, T=131072, Hkv=4, median=0.02, sigma=1.0, cap=0.25):
 def attention_flops(selected_head_blocks, D=128):
     """Algorithmic FLOPs: 4*64*64*D per (query head, selected 64-key block)."""
     return 4.0 * BLOCK * BLOCK * D * selected_head_blocks
+
+
+def cfg3_gate_weights(seed=0, D=128, P=128):
+    """Selector gate projections Wq, Wk [D, P] float32, Xavier-uniform, seeded.
+
+    Laid out as FlatGate's per-layer weights (x @ W)."""
+    gen = torch.Generator().manual_seed(seed + 3)
+    Wq = torch.empty(D, P)
+    Wk = torch.empty(D, P)
+    torch.nn.init.xavier_uniform_(Wq, generator=gen)
+    torch.nn.init.xavier_uniform_(Wk, generator=gen)
+    return Wq, Wk
+
+
+def selector_bytes(T, Hq, Hkv, D, top_k, elem_bytes=2):
+    """Compulsory HBM bytes of the selector front end: read Q and K once, write
+    the selected indices."""
+    nb = (T + BLOCK - 1) // BLOCK
+    return (Hq + Hkv) * T * D * elem_bytes + Hkv * nb * top_k * 4

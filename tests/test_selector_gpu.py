@@ -1,0 +1,115 @@
+"""Selector kernels (through the C ABI) against the C oracle, bit for bit.
+
+Pooled summaries, projections, scores and the selected block indices must be
+identical to oracle/selector.c (the same IEEE float32 operation order); the
+full cfg3 workload (T=65536, 28/4 heads, d=128, top-32) is checked end to end.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle.selector as osel
+from selector.gate import FlatGate
+from selector.select import causal_topk_blocks, gate_scores, pool_blocks, project, select_blocks
+from spruce_hip import workloads
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,T,D,dtype", [
+    (1, 28, 4, 1000, 128, torch.bfloat16),
+    (2, 8, 2, 200, 64, torch.float16),
+    (1, 4, 4, 64, 128, torch.float32),
+    (1, 12, 2, 129, 16, torch.bfloat16),
+])
+def test_pooling_is_bit_exact(B, Hq, Hkv, T, D, dtype):
+    gen = torch.Generator().manual_seed(T + D)
+    q = torch.randn(B, T, Hq, D, generator=gen).to(dtype).transpose(1, 2)   # strided view
+    k = torch.randn(B, Hkv, T, D, generator=gen).to(dtype)
+    qm, ks = pool_blocks(q.transpose(1, 2).contiguous().to(DEV).transpose(1, 2), k.to(DEV))
+    eqm, eks = osel.block_pool(q.float().numpy(), k.float().numpy())
+    assert np.array_equal(_np(qm), eqm)
+    assert np.array_equal(_np(ks), eks)
+
+
+def test_projection_scores_and_topk_are_bit_exact():
+    gen = torch.Generator().manual_seed(7)
+    S, Qb, Pq, Pk, D, P = 3, 77, 2, 3, 96, 64
+    qf = torch.randn(S, Qb, Pq, D, generator=gen)
+    kf = torch.randn(S, Qb, Pk, D, generator=gen)
+    Wq = torch.randn(D, P, generator=gen) * 0.1
+    Wk = torch.randn(D, P, generator=gen) * 0.1
+    qp, kp = project(qf.to(DEV), Wq), project(kf.to(DEV), Wk)
+    eqp, ekp = osel.project(qf.numpy(), Wq.numpy()), osel.project(kf.numpy(), Wk.numpy())
+    assert np.array_equal(_np(qp), eqp) and np.array_equal(_np(kp), ekp)
+    for causal in (True, False):
+        s = gate_scores(qp, kp, causal=causal)
+        es = osel.scores(eqp, ekp, causal=causal)
+        assert np.array_equal(_np(s), es), causal
+    sel = causal_topk_blocks(gate_scores(qp, kp), 5)
+    assert np.array_equal(_np(sel), osel.topk(osel.scores(eqp, ekp), 5))
+
+
+def test_topk_ties_short_rows_and_negative_zero():
+    gen = torch.Generator().manual_seed(11)
+    s = torch.randn(2, 300, 300, generator=gen)
+    s[0, 250, :251] = 1.5                      # all tied: lowest indices win
+    s[0, 120, [4, 50, 99, 100]] = 9.0          # tie at the top
+    s[1, 200, :201] = 0.0
+    s[1, 200, ::2] = -0.0                      # +0 / -0 tie, treated as equal
+    s[1, 280, 17] = float("inf")
+    got = causal_topk_blocks(s.to(DEV), 32)
+    exp = osel.topk(s.numpy(), 32)
+    assert np.array_equal(_np(got), exp)
+    assert _np(got)[0, 250].tolist() == list(range(32))
+    assert _np(got)[0, 10].tolist() == list(range(11)) + [-1] * 21
+
+
+def test_flat_gate_matches_reference_bruteforce():
+    # Reference tests/test_gate_maxsim.py:22-33 on the HIP scorer.
+    torch.manual_seed(0)
+    L, G, qb, kb, P, d = 2, 2, 3, 3, 4, 8
+    gate = FlatGate(L, d, proj_dim=d).eval()
+    q = torch.randn(L, G, qb, P, d)
+    k = torch.randn(L, G, kb, P, d)
+    with torch.no_grad():
+        s = gate.to(DEV)(q.to(DEV), k.to(DEV))
+        qp = torch.einsum("lgqid,ldp->lgqip", q.double(), gate.Wq.cpu().double())
+        kp = torch.einsum("lgkjd,ldp->lgkjp", k.double(), gate.Wk.cpu().double())
+        ref = torch.einsum("lgqip,lgkjp->lgqkij", qp, kp).amax(dim=(-1, -2)) / gate.proj_dim ** 0.5
+    assert s.shape == (L, G, qb, kb)
+    torch.testing.assert_close(s.cpu().double(), ref, atol=1e-5, rtol=1e-5)
+    with pytest.raises(RuntimeError, match="no_grad"):
+        gate(q.to(DEV), k.to(DEV))
+
+
+def test_cfg3_full_size_selected_blocks_bit_exact():
+    # BASELINE cfg3: T=65536 (1024 key blocks), 28 Q / 4 KV heads, d=128, bf16, top-32.
+    print("cfg3: generating inputs", flush=True)
+    q, k, _ = workloads.qkv(0, 65536, 28, 4, 128, torch.bfloat16, use_rope=False, layout="bthd")
+    Wq, Wk = workloads.cfg3_gate_weights(0)
+    got = select_blocks(q.transpose(1, 2).contiguous().to(DEV).transpose(1, 2), k.to(DEV),
+                        Wq.to(DEV), Wk.to(DEV), top_k=32, return_intermediates=True)
+    torch.cuda.synchronize()
+    print("cfg3: oracle", flush=True)
+    exp = osel.flat_select(q.float().numpy(), k.float().numpy(), Wq.numpy(), Wk.numpy(), top_k=32)
+    for name in ("q_mean", "k_sum", "scores"):
+        assert np.array_equal(_np(got[name]), exp[name]), name
+    assert np.array_equal(_np(got["qp"]), exp["qp"][:, :, :, 0])
+    assert np.array_equal(_np(got["kp"]), exp["kp"])
+    sel = _np(got["selected"])
+    assert sel.shape == (1, 1, 4, 1024, 32) and sel.dtype == np.int32
+    assert np.array_equal(sel, exp["selected"])
+    # Contract: causal, strictly increasing, trailing -1 padding, full rows after block 31.
+    rows = sel[0, 0].reshape(-1, 32)
+    valid = rows >= 0
+    assert np.all(rows[valid] <= np.repeat(np.arange(1024)[None], 4, 0).reshape(-1, 1).repeat(32, 1)[valid])
+    both = valid[:, 1:] & valid[:, :-1]
+    assert np.all(np.diff(rows, axis=1)[both] > 0)              # strictly increasing
+    assert np.all(~valid[:, 1:] | valid[:, :-1])                # padding only trailing
+    assert valid.reshape(4, 1024, 32)[:, 31:].all()             # >= 32 causal blocks: full rows
