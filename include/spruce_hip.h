@@ -174,6 +174,45 @@ int spruce_gate_scores(const float* qp, const float* kp, int64_t S, int64_t Qb, 
 int spruce_causal_topk(const float* scores, int64_t R, int64_t Qb, int64_t Kb, int64_t k, int32_t* out,
                        void* stream);
 
+/* ------------------------------------------------------------------------
+ * Teacher target extraction.
+ * ---------------------------------------------------------------------- */
+
+/* Bytes of device workspace spruce_teacher_block_mass needs:
+ * row statistics [B, Hq, T, 2] plus per-half tile partials [B, Hq, 2, Qb, Qb]
+ * float32, Qb = ceil(T/64). */
+size_t spruce_teacher_workspace_bytes(int64_t B, int64_t Hq, int64_t T);
+
+/*
+ * Dense causal softmax attention reduced to block probability mass without
+ * forming the [T, T] matrix: mass[b][h][I][J] = sum over query rows i of
+ * block I and keys j <= i of block J of softmax_j(q_i . k_j * scale), with
+ * query head h reading KV head h / (Hq/Hkv); 0 for J > I.
+ * Replaces chunked_pool (teacher/chunked_extract.py:91-131) with the GQA
+ * repetition of _repeat_kv (:83-88) folded in.
+ *   q [B, Hq, T, D], k [B, Hkv, T, D] (strides as for the attention entry
+ *   points), mass float32 [B, Hq, Qb, Qb] contiguous, D in {64, 128}.
+ * Rows of mass sum to the number of real query rows of the block (64).
+ */
+int spruce_teacher_block_mass(const void* q, const int64_t qs[4], const void* k, const int64_t ks[4],
+                              int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D, float scale,
+                              int dtype, float* mass, float* workspace, size_t workspace_bytes,
+                              void* stream);
+
+/*
+ * Teacher targets from block mass (load_teacher, selector/targets.py:104-121,
+ * and the top-k targets of selector/loss.py:34-46): per (b, KV head g, query
+ * block i) the mean of mass over the group's query heads, zero above the
+ * diagonal, row_mass = its row sum, target = mass / max(row_mass, eps), and
+ * topk = the k causal blocks with the largest target, ordered by target
+ * descending (ties to the lower block index), -1 padding for short rows.
+ *   mass [B, Hq, Qb, Kb] -> target [B, Hkv, Qb, Kb], row_mass [B, Hkv, Qb],
+ *   topk int32 [B, Hkv, Qb, k]; all contiguous; 1 <= k <= 64, Kb <= 8192.
+ */
+int spruce_teacher_targets(const float* mass, int64_t B, int64_t Hq, int64_t Hkv, int64_t Qb, int64_t Kb,
+                           int64_t k, float eps, float* target, float* row_mass, int32_t* topk,
+                           void* stream);
+
 /*
  * Launch configuration the attention entry points use for a shape, as JSON:
  * {"variant":..,"best_config":{..}}.  Replaces kernel_runtime_metadata

@@ -1,0 +1,414 @@
+// Teacher target extraction on gfx950: dense causal softmax attention reduced
+// to per-(head, query block, key block) probability mass, without ever forming
+// the [T, T] attention matrix, and the row-normalised top-k block targets.
+//
+// Semantics follow chunked_pool (teacher/chunked_extract.py:91-131):
+//   mass[b, h, I, J] = sum over query rows i of block I and keys j of block J,
+//   j <= i, of softmax_j(q_i . k_j * scale) over the row's causal keys,
+// with query head h reading KV head h / G (the reference repeats K to H heads,
+// teacher/chunked_extract.py:83-88,139), and the target post-processing of
+// load_teacher (selector/targets.py:104-121): mean over the G query heads of a
+// KV group, causal mask, row normalisation with eps, plus the top-k blocks of
+// each target row (selector/loss.py:34-46, selector/recall.py:35).
+//
+// Scores are computed in float32 from bf16/f16 MFMA inputs (the reference
+// rounds QK^T to the model dtype before its float32 softmax,
+// teacher/chunked_extract.py:119,126).
+//
+// Two passes over the causal (I, J) tiles, GQA-packed like the sparse prefill
+// kernel (one workgroup per (batch, KV head, query block, part), one 32-row
+// tile of one query head per wave, K blocks staged once per workgroup in LDS):
+//   pass 1: running row max and softmax denominator per query row;
+//   pass 2: recomputed scores -> exp(s - m) / l summed over each 64x64 tile,
+//           one float per (tile half, J) into a [B, H, 2, Qb, Qb] workspace;
+//   combine: mass = half0 + half1 (exactly two addends, order-independent).
+#include "attention_impl.h"
+
+namespace spruce {
+
+struct MassParams {
+  const void* q;
+  const void* k;
+  int64_t qs[4], ks[4];
+  int B, Hq, Hkv, T, G, Qb, parts;
+  float cs;     // scale * log2(e)
+  float* stats;  // [B, Hq, T, 2]: (row max in log2 units, row sum)
+  float* part;   // [B, Hq, 2, Qb, Qb]
+};
+
+template <int D, int WAVES, typename TIn, bool F16, int PASS>
+__global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams p) {
+  constexpr int NTHR = WAVES * 64;
+  constexpr int KSTR = D + 8;
+  constexpr int KTILE = kBlock * KSTR;
+  constexpr int KROWCH = D / 8;
+  constexpr int KCHUNKS = kBlock * KROWCH;
+  constexpr int KCH = (KCHUNKS + NTHR - 1) / NTHR;
+  constexpr int KS = D / 16;
+  constexpr int EB = TIn::bytes;
+
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * KTILE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hl = lane >> 5;
+
+  const int nrows = p.B * p.Hkv * p.Qb;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int chunk = slot / p.parts;
+  const int part = slot - chunk * p.parts;
+  const int roww = chunk * 8 + xcd;
+  if (roww >= nrows) return;
+  const int bh = p.B * p.Hkv;
+  const int qb = p.Qb - 1 - roww / bh;  // heaviest rows first
+  const int bg = roww - (roww / bh) * bh;
+  const int b = bg / p.Hkv, g = bg - (bg / p.Hkv) * p.Hkv;
+  const int tile = part * WAVES + wave;
+  const bool active = tile < 2 * p.G;
+  const int hq = active ? (tile >> 1) : 0;
+  const int head = g * p.G + hq;
+  const int half = tile & 1;
+  const int q0 = qb * kBlock + half * 32;
+  const int qin = half * 32 + l32;
+  const int qtok = q0 + l32;
+
+  uint4 qf[KS];
+  {
+    const int qrs = (int)(p.qs[2] * EB);
+    int nq = p.T - q0;
+    nq = nq < 0 ? 0 : (nq > 32 ? 32 : nq);
+    if (!active) nq = 0;
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(
+        static_cast<const char*>(p.q) + ((int64_t)b * p.qs[0] + (int64_t)head * p.qs[1] + (int64_t)q0 * p.qs[2]) * EB,
+        (uint32_t)(nq * qrs));
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk)
+      qf[kk] = raw_to_mfma<TIn, F16>(buf_load8<TIn>(rq, l32 * qrs + (16 * kk + 8 * hl) * EB));
+  }
+
+  const char* kbase = static_cast<const char*>(p.k) + ((int64_t)b * p.ks[0] + (int64_t)g * p.ks[1]) * EB;
+  const int krs = (int)(p.ks[2] * EB);
+  static_assert(NTHR % KROWCH == 0, "staging layout");
+  constexpr int KRP = NTHR / KROWCH;
+  const int key0 = tid / KROWCH, dc0 = tid % KROWCH;
+  const int koff0 = key0 * krs + dc0 * 8 * EB, klds0 = key0 * KSTR + dc0 * 8;
+  raw8_t<TIn> kst[KCH];
+  auto load_k = [&](int blk) {
+    int nk = p.T - blk * kBlock;
+    nk = nk > kBlock ? kBlock : nk;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + (int64_t)blk * kBlock * krs, (uint32_t)(nk * krs));
+#pragma unroll
+    for (int i = 0; i < KCH; ++i)
+      kst[i] = buf_load8<TIn>(rk, key0 + i * KRP < kBlock ? koff0 + i * KRP * krs : kOutOfRange);
+  };
+  auto store_k = [&](int buf) {
+    uint16_t* Ks = smem + buf * KTILE;
+#pragma unroll
+    for (int i = 0; i < KCH; ++i)
+      if ((KCHUNKS % NTHR) == 0 || key0 + i * KRP < kBlock)
+        *reinterpret_cast<uint4*>(Ks + klds0 + i * KRP * KSTR) = raw_to_mfma<TIn, F16>(kst[i]);
+  };
+
+  // Row statistics (pass 1 accumulates them; pass 2 reads them).
+  float m_use = -INFINITY, l_run = 0.f, inv_l = 0.f;
+  float* stat = p.stats + (((int64_t)b * p.Hq + head) * p.T + (qtok < p.T ? qtok : 0)) * 2;
+  if (PASS == 2 && active && qtok < p.T) {
+    m_use = stat[0];
+    inv_l = 1.f / stat[1];
+  }
+  float* part_out = p.part + ((((int64_t)b * p.Hq + head) * 2 + half) * p.Qb + qb) * p.Qb;
+
+  load_k(0);
+  store_k(0);
+  __syncthreads();
+  int buf = 0;
+  for (int J = 0; J <= qb; ++J) {
+    const bool more = J < qb;
+    if (more) load_k(J + 1);
+    if (active) {
+      const uint16_t* kp = smem + buf * KTILE + l32 * KSTR + 8 * hl;
+      f32x16_t s0 = f32x16_t{}, s1 = f32x16_t{};
+      uint4 a0 = *reinterpret_cast<const uint4*>(kp);
+      uint4 a1 = *reinterpret_cast<const uint4*>(kp + 32 * KSTR);
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) {
+        uint4 n0 = a0, n1 = a1;
+        if (kk + 1 < KS) {
+          n0 = *reinterpret_cast<const uint4*>(kp + 16 * (kk + 1));
+          n1 = *reinterpret_cast<const uint4*>(kp + 32 * KSTR + 16 * (kk + 1));
+        }
+        s0 = mfma32x32x16<F16>(a0, qf[kk], s0);
+        s1 = mfma32x32x16<F16>(a1, qf[kk], s1);
+        a0 = n0;
+        a1 = n1;
+      }
+      if (J == qb) {
+        const int thr = qin - 4 * hl;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kr = 8 * (r >> 2) + (r & 3);
+          if (kr > thr) s0[r] = -INFINITY;
+          if (32 + kr > thr) s1[r] = -INFINITY;
+        }
+      }
+      if (PASS == 1) {
+        float mx = fmaxf(s0[0], s0[1]);
+#pragma unroll
+        for (int r = 2; r < 16; ++r) mx = fmaxf(mx, s0[r]);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s1[r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float cand = mx * p.cs;
+        if (__ballot(cand > m_use + kRescaleThreshold) != 0) {
+          const float m_new = fmaxf(m_use, cand);
+          l_run *= fast_exp2(m_use - m_new);
+          m_use = m_new;
+        }
+        const float nm = -m_use;
+        float ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ps += fast_exp2(fmaf(s0[r], p.cs, nm)) + fast_exp2(fmaf(s1[r], p.cs, nm));
+        l_run += ps;
+      } else {
+        const float nm = -m_use;
+        float ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ps += fast_exp2(fmaf(s0[r], p.cs, nm)) + fast_exp2(fmaf(s1[r], p.cs, nm));
+        float v = (qtok < p.T) ? ps * inv_l : 0.f;
+        // Sum over the wave's 32 query rows x 64 keys (fixed butterfly order).
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+        if (lane == 0) part_out[J] = v;
+      }
+    }
+    if (!more) break;
+    store_k(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+  if (PASS == 1 && active) {
+    const float lt = l_run + __shfl_xor(l_run, 32);
+    if (hl == 0 && qtok < p.T) {
+      stat[0] = m_use;
+      stat[1] = lt;
+    }
+  }
+}
+
+// mass[b,h,I,J] = part[b,h,0,I,J] + part[b,h,1,I,J] for J <= I, 0 above.
+__global__ __launch_bounds__(256) void mass_combine_kernel(const float* __restrict__ part, int64_t slabs, int Qb,
+                                                           float* __restrict__ mass) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t per = (int64_t)Qb * Qb;
+  if (idx >= slabs * per) return;
+  const int64_t s = idx / per;
+  const int64_t r = idx - s * per;
+  const int I = (int)(r / Qb), J = (int)(r - (int64_t)(r / Qb) * Qb);
+  const float* p0 = part + s * 2 * per;
+  mass[idx] = J <= I ? p0[r] + p0[per + r] : 0.f;
+}
+
+__device__ __forceinline__ uint32_t target_key(float f) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, f + 0.0f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Per (batch, KV head, query block) row: mean over the group's query heads,
+// causal mask, row normalisation, then the k largest targets (descending,
+// ties to the lower block index; -1 padding for short causal rows).
+constexpr int kTgtMaxKb = 8192;
+__global__ __launch_bounds__(256) void teacher_targets_kernel(const float* __restrict__ mass, int Hq, int Hkv,
+                                                              int Qb, int Kb, int k, float eps,
+                                                              float* __restrict__ target, float* __restrict__ row_mass,
+                                                              int32_t* __restrict__ topk) {
+  __shared__ float vals[kTgtMaxKb];
+  __shared__ float red[256];
+  __shared__ int hist[256];
+  __shared__ int sel_bin, sel_rem;
+  __shared__ int sel_idx[64];
+  __shared__ uint32_t sel_key[64];
+  const int tid = threadIdx.x;
+  const int row = blockIdx.x;  // (b*Hkv + g)*Qb + i
+  const int i = row % Qb;
+  const int bg = row / Qb;
+  const int g = bg % Hkv, b = bg / Hkv;
+  const int G = Hq / Hkv;
+  const int n = i + 1 < Kb ? i + 1 : Kb;
+  float part = 0.f;
+  for (int j = tid; j < Kb; j += 256) {
+    float v = 0.f;
+    if (j < n) {
+      for (int h = 0; h < G; ++h) v += mass[((((int64_t)b * Hq + g * G + h) * Qb) + i) * Kb + j];
+      v = v / (float)G;
+    }
+    vals[j] = v;
+    part += v;
+  }
+  red[tid] = part;
+  __syncthreads();
+  for (int st = 128; st >= 1; st >>= 1) {
+    if (tid < st) red[tid] += red[tid + st];
+    __syncthreads();
+  }
+  const float rs = red[0];
+  const float den = rs > eps ? rs : eps;
+  float* trow = target + (int64_t)row * Kb;
+  for (int j = tid; j < Kb; j += 256) {
+    const float t = vals[j] / den;
+    trow[j] = t;
+    vals[j] = t;
+  }
+  if (tid == 0) row_mass[row] = rs;
+  __syncthreads();
+  int32_t* o = topk + (int64_t)row * k;
+  const int m = n < k ? n : k;
+  // Radix select of the m-th largest target key among the causal entries.
+  uint32_t prefix = 0, mask = 0;
+  int rem = m;
+  for (int pass = 3; pass >= 0; --pass) {
+    hist[tid] = 0;
+    __syncthreads();
+    const int sh = 8 * pass;
+    for (int j = tid; j < n; j += 256) {
+      const uint32_t key = target_key(vals[j]);
+      if ((key & mask) == prefix) atomicAdd(&hist[(key >> sh) & 255], 1);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      int cum = 0, bin = 0;
+      for (int bb = 255; bb >= 0; --bb) {
+        if (cum + hist[bb] >= rem) {
+          bin = bb;
+          break;
+        }
+        cum += hist[bb];
+      }
+      sel_bin = bin;
+      sel_rem = rem - cum;
+    }
+    __syncthreads();
+    prefix |= (uint32_t)sel_bin << sh;
+    mask |= 255u << sh;
+    rem = sel_rem;
+    __syncthreads();
+  }
+  if (tid < 64) {
+    int eq_base = 0, out_base = 0;
+    const uint64_t lt = (tid == 0) ? 0ull : (~0ull >> (64 - tid));
+    for (int c0 = 0; c0 < n; c0 += 64) {
+      const int j = c0 + tid;
+      const uint32_t key = j < n ? target_key(vals[j]) : 0u;
+      const bool eq = j < n && key == prefix;
+      const uint64_t eqb = __ballot(eq);
+      const int rank = eq_base + __popcll(eqb & lt);
+      const bool sel = j < n && (key > prefix || (eq && rank < rem));
+      const uint64_t sb = __ballot(sel);
+      if (sel) {
+        const int pos = out_base + __popcll(sb & lt);
+        sel_idx[pos] = j;
+        sel_key[pos] = key;
+      }
+      eq_base += __popcll(eqb);
+      out_base += __popcll(sb);
+    }
+    // Order the m selected entries by target descending, index ascending.
+    if (tid < m) {
+      const uint32_t key = sel_key[tid];
+      const int idx = sel_idx[tid];
+      int rank = 0;
+      for (int t = 0; t < m; ++t) rank += (sel_key[t] > key) || (sel_key[t] == key && sel_idx[t] < idx);
+      o[rank] = idx;
+    }
+    if (tid >= m && tid < k) o[tid] = -1;
+  }
+}
+
+template <int D, typename TIn, bool F16, int PASS>
+int launch_mass_w(const MassParams& p, int waves, hipStream_t s) {
+  const int64_t grid = ((int64_t)p.B * p.Hkv * p.Qb + 7) / 8 * 8 * p.parts;
+  switch (waves) {
+    case 2: hipLaunchKernelGGL((block_mass_kernel<D, 2, TIn, F16, PASS>), dim3((unsigned)grid), dim3(128), 0, s, p); break;
+    case 4: hipLaunchKernelGGL((block_mass_kernel<D, 4, TIn, F16, PASS>), dim3((unsigned)grid), dim3(256), 0, s, p); break;
+    case 7: hipLaunchKernelGGL((block_mass_kernel<D, 7, TIn, F16, PASS>), dim3((unsigned)grid), dim3(448), 0, s, p); break;
+    case 8: hipLaunchKernelGGL((block_mass_kernel<D, 8, TIn, F16, PASS>), dim3((unsigned)grid), dim3(512), 0, s, p); break;
+    default: return set_error(SPRUCE_EINVAL, "unsupported wave count %d", waves);
+  }
+  return check_launch("block_mass_kernel");
+}
+
+template <int PASS>
+int launch_mass(const MassParams& p, int D, int dtype, int waves, hipStream_t s) {
+  if (D == 128) {
+    if (dtype == SPRUCE_DTYPE_BF16) return launch_mass_w<128, InBF16, false, PASS>(p, waves, s);
+    if (dtype == SPRUCE_DTYPE_F16) return launch_mass_w<128, InF16, true, PASS>(p, waves, s);
+    return launch_mass_w<128, InF32, false, PASS>(p, waves, s);
+  }
+  if (dtype == SPRUCE_DTYPE_BF16) return launch_mass_w<64, InBF16, false, PASS>(p, waves, s);
+  if (dtype == SPRUCE_DTYPE_F16) return launch_mass_w<64, InF16, true, PASS>(p, waves, s);
+  return launch_mass_w<64, InF32, false, PASS>(p, waves, s);
+}
+
+}  // namespace spruce
+
+using namespace spruce;
+
+extern "C" int spruce_teacher_block_mass(const void* q, const int64_t qs[4], const void* k, const int64_t ks[4],
+                                         int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D, float scale,
+                                         int dtype, float* mass, float* workspace, size_t workspace_bytes,
+                                         void* stream) {
+  // Reuse the attention argument checks (v aliases k; out only needs alignment).
+  AttnParams ap;
+  LaunchShape shape;
+  const int64_t fake_os[4] = {0, 0, 4, 1};
+  int rc = prepare_attention(ap, q, qs, k, ks, k, ks, B, Hq, Hkv, T, D, scale, dtype, SPRUCE_VARIANT_SINGLE_HEAD,
+                             mass, fake_os, shape);
+  if (rc) return rc;
+  SPRUCE_REQUIRE(mass != nullptr && workspace != nullptr, "mass and workspace must be non-null");
+  const int64_t Qb = (T + kBlock - 1) / kBlock;
+  const size_t need = spruce_teacher_workspace_bytes(B, Hq, T);
+  SPRUCE_REQUIRE(workspace_bytes >= need, "workspace too small: %zu bytes, need %zu", workspace_bytes, need);
+  SPRUCE_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, "workspace must be 16-byte aligned");
+  MassParams p{};
+  p.q = q;
+  p.k = k;
+  for (int i = 0; i < 4; ++i) {
+    p.qs[i] = qs[i];
+    p.ks[i] = ks[i];
+  }
+  p.B = (int)B;
+  p.Hq = (int)Hq;
+  p.Hkv = (int)Hkv;
+  p.T = (int)T;
+  p.G = (int)(Hq / Hkv);
+  p.Qb = (int)Qb;
+  p.parts = shape.parts;
+  p.cs = scale * 1.4426950408889634f;
+  p.stats = workspace;
+  p.part = workspace + (size_t)B * Hq * T * 2;
+  hipStream_t s = (hipStream_t)stream;
+  rc = launch_mass<1>(p, (int)D, dtype, shape.waves, s);
+  if (rc) return rc;
+  rc = launch_mass<2>(p, (int)D, dtype, shape.waves, s);
+  if (rc) return rc;
+  const int64_t total = B * Hq * Qb * Qb;
+  hipLaunchKernelGGL(mass_combine_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, p.part, B * Hq,
+                     (int)Qb, mass);
+  return check_launch("mass_combine_kernel");
+}
+
+extern "C" size_t spruce_teacher_workspace_bytes(int64_t B, int64_t Hq, int64_t T) {
+  const int64_t Qb = (T + kBlock - 1) / kBlock;
+  return (size_t)(B * Hq * T * 2 + B * Hq * 2 * Qb * Qb) * sizeof(float);
+}
+
+extern "C" int spruce_teacher_targets(const float* mass, int64_t B, int64_t Hq, int64_t Hkv, int64_t Qb, int64_t Kb,
+                                      int64_t k, float eps, float* target, float* row_mass, int32_t* topk,
+                                      void* stream) {
+  SPRUCE_REQUIRE(mass && target && row_mass && topk, "mass, target, row_mass and topk must be non-null");
+  SPRUCE_REQUIRE(B >= 1 && Hkv >= 1 && Hq >= Hkv && Hq % Hkv == 0 && Qb >= 1 && Kb >= 1, "invalid shape");
+  SPRUCE_REQUIRE(k >= 1 && k <= 64, "k must be in [1, 64], got %lld", (long long)k);
+  SPRUCE_REQUIRE(Kb <= kTgtMaxKb, "at most %d key blocks per row are supported", kTgtMaxKb);
+  SPRUCE_REQUIRE(B * Hkv * Qb < ((int64_t)1 << 31), "too many rows");
+  hipLaunchKernelGGL(teacher_targets_kernel, dim3((unsigned)(B * Hkv * Qb)), dim3(256), 0, (hipStream_t)stream, mass,
+                     (int)Hq, (int)Hkv, (int)Qb, (int)Kb, (int)k, eps, target, row_mass, topk);
+  return check_launch("teacher_targets_kernel");
+}

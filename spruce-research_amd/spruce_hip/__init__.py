@@ -49,6 +49,11 @@ _SIGNATURES = {
     "spruce_gate_project": [_p, _p, _i64, _i64, _i64, _p, _p],
     "spruce_gate_scores": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int, _p, _p],
     "spruce_causal_topk": [_p, _i64, _i64, _i64, _i64, _p, _p],
+    "spruce_teacher_block_mass": [
+        _p, _STRIDES, _p, _STRIDES, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int,
+        _p, _p, ctypes.c_size_t, _p],
+    "spruce_teacher_targets": [
+        _p, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _p, _p, _p, _p],
     "spruce_sparse_prefill_mask": [
         _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _i64,
         _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int, ctypes.c_int,
@@ -77,6 +82,8 @@ def lib():
             fn.restype = ctypes.c_int
         handle.spruce_version.restype = ctypes.c_char_p
         handle.spruce_version.argtypes = []
+        handle.spruce_teacher_workspace_bytes.restype = ctypes.c_size_t
+        handle.spruce_teacher_workspace_bytes.argtypes = [_i64, _i64, _i64]
         _lib = handle
     return _lib
 

@@ -167,3 +167,9 @@ def selector_bytes(T, Hq, Hkv, D, top_k, elem_bytes=2):
     the selected indices."""
     nb = (T + BLOCK - 1) // BLOCK
     return (Hq + Hkv) * T * D * elem_bytes + Hkv * nb * top_k * 4
+
+
+def teacher_flops(T, H, block=BLOCK, D=128):
+    """Algorithmic FLOPs of teacher mass: 2*64*64*D per (query head, causal block pair)."""
+    qb = (T + block - 1) // block
+    return 2.0 * block * block * D * H * qb * (qb + 1) // 2
