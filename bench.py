@@ -12,8 +12,9 @@ Printed: one JSON line with the BASELINE metric (effective TFLOP/s over the
 computed blocks, 4*64*64*128 FLOP per (query head, selected block)), ms per
 step, the live roofline of the kernel (HIP events on the launch stream) and a
 CPU baseline (the float32 numpy oracle on a bounded sample of the same
-workload).  The 128K direct-index CSR configuration (BASELINE cfg5) is timed
-the same way and reported under "configs".
+workload).  The 128K direct-index CSR configuration (BASELINE cfg5), the
+selector front end (cfg3, HBM-bound: GB/s) and teacher block-mass extraction
+(cfg4) are timed the same way and reported under "configs".
 """
 import argparse
 import json
@@ -104,6 +105,7 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-csr128k", action="store_true", help="skip the 128K CSR configuration")
+    ap.add_argument("--no-extra", action="store_true", help="skip the selector (cfg3) and teacher (cfg4) legs")
     ap.add_argument("--calib-copy", action="store_true",
                     help="after timing, run one plain 512 MiB device copy (PMC byte calibration)")
     args = ap.parse_args()
@@ -169,6 +171,46 @@ def main():
             "row_blocks_mean": round(float(counts.mean()), 2), "row_blocks_max": int(counts.max()),
         }
         del q5, k5, v5
+
+    # ---- cfg3: selector front end, T=65536 (1024 key blocks), top-32
+    if not args.no_extra:
+        from selector.select import select_blocks
+        T3 = 65536
+        q3, k3, _ = workloads.qkv(args.seed, T3, Hq, Hkv, D, torch.bfloat16, use_rope=False,
+                                  layout="bthd", device="cuda")
+        Wq, Wk = (w.to(dev) for w in workloads.cfg3_gate_weights(args.seed))
+        fn3 = lambda: select_blocks(q3, k3, Wq, Wk, top_k=32)  # noqa: E731
+        _, k3ms = _time_launches(fn3, max(10, args.steps // 2), max(3, args.warmup // 2))
+        m3 = statistics.median(k3ms)
+        by3 = workloads.selector_bytes(T3, Hq, Hkv, D, 32)
+        configs["cfg3_selector_64k"] = {
+            "ms_median": round(m3, 4), "ms_min": round(min(k3ms), 4), "ms_max": round(max(k3ms), 4),
+            "gbps": round(by3 / (m3 * 1e-3) / 1e9, 1),
+            "frac_hbm_peak": round(by3 / (m3 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "compulsory_bytes": by3, "top_k": 32,
+            "stages": "pool (Q group+block mean, K mean/max) -> project -> MaxSim scores -> causal top-k",
+        }
+        del q3, k3
+
+    # ---- cfg4: teacher block mass + targets, T=16384 (256 blocks)
+    if not args.no_extra:
+        from teacher.chunked_extract import chunked_pool
+        from teacher.targets import teacher_targets
+        T4 = 16384
+        q4, k4, _ = workloads.qkv(args.seed, T4, Hq, Hkv, D, torch.bfloat16, use_rope=True,
+                                  layout="bthd", device="cuda")
+        fn4 = lambda: teacher_targets(chunked_pool(q4, k4, scale), Hkv, k=8)  # noqa: E731
+        _, k4ms = _time_launches(fn4, max(10, args.steps // 2), max(3, args.warmup // 2))
+        m4 = statistics.median(k4ms)
+        fl4 = workloads.teacher_flops(T4, Hq)
+        configs["cfg4_teacher_16k"] = {
+            "ms_median": round(m4, 4), "ms_min": round(min(k4ms), 4), "ms_max": round(max(k4ms), 4),
+            "tflops": round(fl4 / (m4 * 1e-3) / 1e12, 2),
+            "frac_bf16_peak": round(fl4 / (m4 * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "flop": fl4, "top_k": 8,
+            "note": "algorithmic FLOP = QK^T once over causal blocks; the kernel runs QK^T twice",
+        }
+        del q4, k4
 
     if args.calib_copy:
         # A plain copy of known size: reads and writes exactly 512 MiB.  Its
