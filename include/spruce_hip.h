@@ -214,6 +214,58 @@ int spruce_teacher_targets(const float* mass, int64_t B, int64_t Hq, int64_t Hkv
                            void* stream);
 
 /*
+ * Selector prototype features in the model dtype.  Replaces _proto_pool_seq
+ * (teacher/chunked_extract.py:27-72) applied to _group_avg_tokens (:75-80):
+ * x [B, H, L, D] (strided, element strides xs) is averaged over the H/G heads
+ * of each group per token (G == H: no averaging), then per block of `block`
+ * tokens prototype 0 is the mean of the real rows and prototypes 1..k,
+ * k = min(P-1, block), are the k rows farthest from it in float32 squared L2
+ * (farthest first, ties to the lower row); slots past the real rows hold the
+ * mean.  out [B, G, ceil(L/block), P, D] contiguous, x's dtype.
+ * Limits: D <= 128, 1 <= block <= 64, 1 <= P <= 65.  Deterministic (fixed
+ * float32 operation order).
+ */
+int spruce_proto_pool(const void* x, const int64_t xs[4], int64_t B, int64_t H, int64_t L, int64_t D,
+                      int64_t G, int64_t block, int64_t P, int dtype, void* out, void* stream);
+
+/*
+ * Per-token group average, x [B, H, L, D] -> out [B, G, L, D] contiguous, x's
+ * dtype.  Replaces _group_avg_tokens (teacher/chunked_extract.py:75-80).
+ */
+int spruce_group_avg_tokens(const void* x, const int64_t xs[4], int64_t B, int64_t H, int64_t L, int64_t D,
+                            int64_t G, int dtype, void* out, void* stream);
+
+/*
+ * Packs compact traversal IDs into selected_blocks rows.  Replaces
+ * selected_ids_to_blocks (scripts/export_selected_blocks.py:79-175), same
+ * policy: forced sink blocks [0, min(sink_blocks, key_blocks)) strictly before
+ * the local window, then the smallest distinct IDs in
+ * [sink, min(q - local_window, key_blocks)) up to the remaining budget, then
+ * the local window q-local_window..q (ids >= 0); ascending, PAD -1.
+ *   ids  [R, C] contiguous, int32 (id_bytes 4) or int64 (id_bytes 8), rows
+ *        ordered (layer, kv head, query block) so q = row % qb; any value
+ *        allowed (out-of-range IDs are ignored, duplicates count once).
+ *   out  int32 [R, out_cols] contiguous; out_cols must equal
+ *        min(k_selected, C + min(sink_blocks, key_blocks) + local_window + 1).
+ * Errors: k_selected < local_window + 1 + sink_blocks, key_blocks < 1 or
+ * > 65536, negative local_window/sink_blocks.
+ */
+int spruce_pack_selected_ids(const void* ids, int id_bytes, int64_t R, int64_t qb, int64_t C,
+                             int64_t key_blocks, int64_t k_selected, int64_t local_window,
+                             int64_t sink_blocks, int32_t* out, int64_t out_cols, void* stream);
+
+/*
+ * Packs a boolean route mask into selected_blocks rows.  Replaces
+ * selected_mask_to_blocks (scripts/export_selected_blocks.py:37-76): the
+ * local window q-local_window..min(q, kb-1) is forced, and the first causal
+ * non-local columns of the row fill the rest of k_selected; ascending, PAD -1.
+ *   mask uint8 [R, kb] contiguous (nonzero = selected), q = row % qb.
+ *   out  int32 [R, out_cols], out_cols = min(k_selected, kb).
+ */
+int spruce_pack_selected_mask(const uint8_t* mask, int64_t R, int64_t qb, int64_t kb, int64_t k_selected,
+                              int64_t local_window, int32_t* out, int64_t out_cols, void* stream);
+
+/*
  * Launch configuration the attention entry points use for a shape, as JSON:
  * {"variant":..,"best_config":{..}}.  Replaces kernel_runtime_metadata
  * (kernels/seerattention_direct_index_triton.py:430-447).

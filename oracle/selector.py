@@ -1,4 +1,4 @@
-"""Selector oracle (ctypes wrapper of oracle/selector.c) -- TEST INFRASTRUCTURE ONLY.
+"""Selector oracle (ctypes wrapper of oracle/selector.c and oracle/proto.c) -- TEST INFRASTRUCTURE ONLY.
 
 The C code fixes the exact float32 operation order the HIP selector kernels
 follow, so pooled summaries, projections, scores and the selected block
@@ -32,7 +32,11 @@ def lib():
         h.oracle_project.argtypes = [_f32p, _f32p, ci, ci, ci, _f32p]
         h.oracle_scores.argtypes = [_f32p, _f32p, ci, ci, ci, ci, ci, ci, ctypes.c_float, ci, _f32p]
         h.oracle_topk.argtypes = [_f32p, ci, ci, ci, ci, _i32p]
-        for f in (h.oracle_block_pool, h.oracle_project, h.oracle_scores, h.oracle_topk):
+        h.oracle_round.argtypes = [_f32p, ctypes.c_int64, ci, _f32p]
+        h.oracle_group_avg.argtypes = [_f32p, ci, ci, ci, ci, ci, ci, _f32p]
+        h.oracle_proto_pool.argtypes = [_f32p, ci, ci, ci, ci, ci, ci, ci, _f32p]
+        for f in (h.oracle_block_pool, h.oracle_project, h.oracle_scores, h.oracle_topk,
+                  h.oracle_round, h.oracle_group_avg, h.oracle_proto_pool):
             f.restype = None
         _lib = h
     return _lib
@@ -106,3 +110,37 @@ def flat_select(q, k, Wq, Wk, top_k=32):
     return {"q_mean": q_mean, "k_sum": k_sum, "qp": qp, "kp": kp,
             "scores": sc.reshape(B, Hkv, nb, nb),
             "selected": sel.reshape(B, Hkv, nb, top_k)[:, None]}
+
+
+DTYPE_CODES = {"bfloat16": 0, "float16": 1, "float32": 2}
+
+
+def round_to(x, dtype):
+    """Nearest-even rounding of float32 values to the model dtype ("bfloat16", "float16", "float32")."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().oracle_round(x.reshape(-1), x.size, DTYPE_CODES[dtype], out.reshape(-1))
+    return out
+
+
+def group_avg(x, G, dtype):
+    """x [B,H,L,D] (model-dtype values as float32) -> [B,G,L,D] (_group_avg_tokens)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    B, H, L, D = x.shape
+    if H % G:
+        raise ValueError(f"H={H} not divisible by G={G}")
+    out = np.zeros((B, G, L, D), np.float32)
+    lib().oracle_group_avg(x, B, H, L, D, G, DTYPE_CODES[dtype], out)
+    return out
+
+
+def proto_pool(a, block, P, dtype):
+    """a [B,G,L,D] -> [B,G,nb,P,D]: mean + the min(P-1, block) farthest rows (_proto_pool_seq)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    B, G, L, D = a.shape
+    if block > 64 or D > 512:
+        raise ValueError("oracle proto_pool supports block <= 64 and D <= 512")
+    nb = (L + block - 1) // block
+    out = np.zeros((B, G, nb, P, D), np.float32)
+    lib().oracle_proto_pool(a, B, G, L, D, block, P, DTYPE_CODES[dtype], out)
+    return out

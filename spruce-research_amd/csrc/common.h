@@ -111,4 +111,24 @@ __device__ __forceinline__ uint4 load8(const void* p, bool valid, float mul, boo
   return r;
 }
 
+// Loads 8 consecutive elements (bf16, f16 or f32 per dtype) starting at
+// element offset elem of base, widened to float.
+__device__ __forceinline__ void load8f(const void* base, int64_t elem, int dtype, float* out) {
+  if (dtype == SPRUCE_DTYPE_F32) {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + elem);
+    const float4 a = p[0], b = p[1];
+    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+    out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+  } else {
+    const uint4 r = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + elem);
+    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+    const bool f16 = dtype == SPRUCE_DTYPE_F16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = f16 ? unpack1<true>(w[i] & 0xffffu) : unpack1<false>(w[i] & 0xffffu);
+      out[2 * i + 1] = f16 ? unpack1<true>(w[i] >> 16) : unpack1<false>(w[i] >> 16);
+    }
+  }
+}
+
 }  // namespace spruce

@@ -1,0 +1,268 @@
+// Selector prototype features, in the model dtype:
+//
+//   group_avg   _group_avg_tokens (teacher/chunked_extract.py:75-80): the H/G
+//               query heads of each KV group averaged per token.
+//   proto_pool  _proto_pool_seq (teacher/chunked_extract.py:27-72) fused with
+//               the group average: per block of `block` tokens, prototype 0 is
+//               the mean over the block's real rows and prototypes 1..k
+//               (k = min(P-1, block)) are the k rows farthest from it in
+//               float32 squared L2, farthest first; slots past the real rows
+//               hold the mean.
+//
+// Arithmetic (compiled without contraction, IEEE division):
+//   group average  rnd(sum_h x_h * fl(1/rep)), heads summed in order from 0.0f
+//                  (torch's GPU mean: float accumulation times the factor
+//                  1/n); rep == 1 copies the row unchanged.
+//   block mean     rnd(rnd(sum_t a_t) / n), tokens summed in order (the
+//                  reference sums in the model dtype, then divides in it).
+//   distance       sum_d (a_d - m_d)^2 in float32, dims in order.
+//   top-k          descending distance, ties to the lower row, NaN largest.
+// rnd() rounds to the model dtype (nearest even); float32 input is exact.
+// One workgroup per (batch, KV group, block); the block tile is held in LDS as
+// float.  HBM-bound: every input element is read once.
+#include "common.h"
+
+namespace spruce {
+namespace {
+
+constexpr int kProtoMaxD = 128;
+constexpr int kProtoMaxBlock = 64;
+constexpr int kProtoMaxP = 65;
+
+struct ProtoParams {
+  const void* x;
+  int64_t xs[4];
+  int B, H, G, L, D, block, P, nb, dtype, rep;
+  float inv_rep;
+  void* out;  // [B, G, nb, P, D] in x's dtype, contiguous
+};
+
+__device__ __forceinline__ float round_to(float v, int dtype) {
+  if (dtype == SPRUCE_DTYPE_BF16) return (float)(__bf16)v;
+  if (dtype == SPRUCE_DTYPE_F16) return (float)(_Float16)v;
+  return v;
+}
+
+__device__ __forceinline__ float load1(const void* base, int64_t elem, int dtype) {
+  if (dtype == SPRUCE_DTYPE_F32) return static_cast<const float*>(base)[elem];
+  const uint32_t bits = static_cast<const uint16_t*>(base)[elem];
+  return dtype == SPRUCE_DTYPE_F16 ? unpack1<true>(bits) : unpack1<false>(bits);
+}
+
+__device__ __forceinline__ void store1(void* base, int64_t elem, int dtype, float v) {
+  if (dtype == SPRUCE_DTYPE_F32) {
+    static_cast<float*>(base)[elem] = v;
+  } else if (dtype == SPRUCE_DTYPE_F16) {
+    static_cast<_Float16*>(base)[elem] = (_Float16)v;
+  } else {
+    static_cast<__bf16*>(base)[elem] = (__bf16)v;
+  }
+}
+
+// Group average of the rep heads starting at head h0 for token t, dims
+// [8c, 8c+8) (vector path) -- written to dst[0..8).
+__device__ __forceinline__ void group_avg8(const ProtoParams& p, int b, int h0, int t, int c, float* dst) {
+  const int64_t e0 = (int64_t)b * p.xs[0] + (int64_t)t * p.xs[2] + 8 * c;
+  float s[8];
+  load8f(p.x, e0 + (int64_t)h0 * p.xs[1], p.dtype, s);
+  if (p.rep > 1) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s[j] = 0.0f + s[j];
+    for (int h = 1; h < p.rep; ++h) {
+      float v[8];
+      load8f(p.x, e0 + (int64_t)(h0 + h) * p.xs[1], p.dtype, v);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s[j] = s[j] + v[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s[j] = round_to(s[j] * p.inv_rep, p.dtype);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) dst[j] = s[j];
+}
+
+__device__ __forceinline__ float group_avg1(const ProtoParams& p, int b, int h0, int t, int d) {
+  const int64_t e0 = (int64_t)b * p.xs[0] + (int64_t)t * p.xs[2] + (int64_t)d * p.xs[3];
+  float s = load1(p.x, e0 + (int64_t)h0 * p.xs[1], p.dtype);
+  if (p.rep == 1) return s;
+  s = 0.0f + s;
+  for (int h = 1; h < p.rep; ++h) s = s + load1(p.x, e0 + (int64_t)(h0 + h) * p.xs[1], p.dtype);
+  return round_to(s * p.inv_rep, p.dtype);
+}
+
+__global__ __launch_bounds__(256) void proto_pool_kernel(ProtoParams p) {
+  __shared__ float tile[kProtoMaxBlock][kProtoMaxD + 1];
+  __shared__ float mean[kProtoMaxD];
+  __shared__ int pick[kProtoMaxP];
+  const int tid = threadIdx.x;
+  const int i = blockIdx.x % p.nb;
+  const int bg = blockIdx.x / p.nb;
+  const int g = bg % p.G;
+  const int b = bg / p.G;
+  const int t0 = i * p.block;
+  const int n = min(p.block, p.L - t0);
+  const int h0 = g * p.rep;
+  const bool vec = (p.D & 7) == 0 && p.xs[3] == 1;
+
+  if (vec) {
+    const int dch = p.D >> 3;
+    for (int e = tid; e < n * dch; e += 256) {
+      const int t = e / dch, c = e - (e / dch) * dch;
+      float v[8];
+      group_avg8(p, b, h0, t0 + t, c, v);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) tile[t][8 * c + j] = v[j];
+    }
+  } else {
+    for (int e = tid; e < n * p.D; e += 256) {
+      const int t = e / p.D, d = e - (e / p.D) * p.D;
+      tile[t][d] = group_avg1(p, b, h0, t0 + t, d);
+    }
+  }
+  __syncthreads();
+
+  if (tid < p.D) {
+    float s = 0.0f;
+    for (int t = 0; t < n; ++t) s = s + tile[t][tid];
+    mean[tid] = round_to(round_to(s, p.dtype) / (float)n, p.dtype);
+  }
+  __syncthreads();
+
+  const int k = min(p.P - 1, p.block);
+  if (tid < 64) {
+    // Lane = row of the block; rows past the real ones rank as -inf.
+    float dist = -__builtin_inff();
+    if (tid < n) {
+      float s = 0.0f;
+      for (int d = 0; d < p.D; ++d) {
+        const float diff = tile[tid][d] - mean[d];
+        s = s + diff * diff;
+      }
+      dist = s;
+    }
+    const bool in_block = tid < p.block;
+    const uint32_t u = __builtin_bit_cast(uint32_t, dist);
+    const uint32_t okey = dist != dist ? 0xffffffffu                    // any NaN ranks above +inf
+                                       : ((u & 0x80000000u) ? ~u : (u | 0x80000000u));
+    bool taken = !in_block;
+    for (int j = 0; j < k; ++j) {
+      uint64_t key = taken ? 0ull : (((uint64_t)okey << 32) | (uint32_t)(63 - tid));
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) {
+        const uint64_t o = __shfl_xor(key, m, 64);
+        key = o > key ? o : key;
+      }
+      const int best = 63 - (int)(key & 63u);
+      if (tid == best) taken = true;
+      if (tid == 0) pick[j] = best;
+    }
+  }
+  __syncthreads();
+
+  const int64_t obase = (((int64_t)b * p.G + g) * p.nb + i) * (int64_t)p.P * p.D;
+  for (int e = tid; e < p.P * p.D; e += 256) {
+    const int pr = e / p.D, d = e - (e / p.D) * p.D;
+    float v = mean[d];
+    if (pr >= 1 && pr <= k) {
+      const int row = pick[pr - 1];
+      if (row < n) v = tile[row][d];
+    }
+    store1(p.out, obase + e, p.dtype, v);
+  }
+}
+
+__global__ __launch_bounds__(256) void group_avg_kernel(ProtoParams p, int64_t total8) {
+  // One thread per (b, g, t, 8-dim chunk) -- vector path only.
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= total8) return;
+  const int dch = p.D >> 3;
+  const int c = (int)(e % dch);
+  const int64_t r = e / dch;
+  const int t = (int)(r % p.L);
+  const int bg = (int)(r / p.L);
+  const int g = bg % p.G, b = bg / p.G;
+  float v[8];
+  group_avg8(p, b, g * p.rep, t, c, v);
+  const int64_t o = r * p.D + 8 * c;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) store1(p.out, o + j, p.dtype, v[j]);
+}
+
+__global__ __launch_bounds__(256) void group_avg_scalar_kernel(ProtoParams p, int64_t total) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= total) return;
+  const int d = (int)(e % p.D);
+  const int64_t r = e / p.D;
+  const int t = (int)(r % p.L);
+  const int bg = (int)(r / p.L);
+  const int g = bg % p.G, b = bg / p.G;
+  store1(p.out, e, p.dtype, group_avg1(p, b, g * p.rep, t, d));
+}
+
+int fill_params(ProtoParams& p, const void* x, const int64_t xs[4], int64_t B, int64_t H, int64_t L, int64_t D,
+                int64_t G, int dtype, void* out) {
+  SPRUCE_REQUIRE(x && xs && out, "x, strides and out must be non-null");
+  SPRUCE_REQUIRE(dtype == SPRUCE_DTYPE_BF16 || dtype == SPRUCE_DTYPE_F16 || dtype == SPRUCE_DTYPE_F32,
+                 "unsupported dtype code %d", dtype);
+  SPRUCE_REQUIRE(B >= 1 && H >= 1 && L >= 1 && D >= 1 && G >= 1, "invalid shape");
+  SPRUCE_REQUIRE(H % G == 0, "H=%lld not divisible by G=%lld", (long long)H, (long long)G);
+  SPRUCE_REQUIRE(B < (1 << 20) && H < (1 << 16) && L < ((int64_t)1 << 30), "shape out of range");
+  for (int i = 0; i < 4; ++i) SPRUCE_REQUIRE(xs[i] >= 0, "negative strides are not supported");
+  const int eb = dtype == SPRUCE_DTYPE_F32 ? 4 : 2;
+  if ((D & 7) == 0 && xs[3] == 1) {
+    SPRUCE_REQUIRE(((uintptr_t)x & 15) == 0 && (xs[0] * eb) % 16 == 0 && (xs[1] * eb) % 16 == 0 &&
+                       (xs[2] * eb) % 16 == 0,
+                   "x with a contiguous last dim must be 16-byte aligned in every row");
+  }
+  p.x = x;
+  for (int i = 0; i < 4; ++i) p.xs[i] = xs[i];
+  p.B = (int)B; p.H = (int)H; p.G = (int)G; p.L = (int)L; p.D = (int)D;
+  p.dtype = dtype;
+  p.rep = (int)(H / G);
+  p.inv_rep = 1.0f / (float)p.rep;
+  p.out = out;
+  return SPRUCE_OK;
+}
+
+}  // namespace
+}  // namespace spruce
+
+using namespace spruce;
+
+extern "C" int spruce_proto_pool(const void* x, const int64_t xs[4], int64_t B, int64_t H, int64_t L, int64_t D,
+                                 int64_t G, int64_t block, int64_t P, int dtype, void* out, void* stream) {
+  ProtoParams p;
+  const int rc = fill_params(p, x, xs, B, H, L, D, G, dtype, out);
+  if (rc) return rc;
+  SPRUCE_REQUIRE(D <= kProtoMaxD, "head_dim must be <= %d, got %lld", kProtoMaxD, (long long)D);
+  SPRUCE_REQUIRE(block >= 1 && block <= kProtoMaxBlock, "block must be in [1, %d], got %lld", kProtoMaxBlock,
+                 (long long)block);
+  SPRUCE_REQUIRE(P >= 1 && P <= kProtoMaxP, "P must be in [1, %d], got %lld", kProtoMaxP, (long long)P);
+  p.block = (int)block;
+  p.P = (int)P;
+  p.nb = (int)((L + block - 1) / block);
+  const int64_t grid = B * G * (int64_t)p.nb;
+  SPRUCE_REQUIRE(grid < ((int64_t)1 << 31), "too many blocks");
+  hipLaunchKernelGGL(proto_pool_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, p);
+  return check_launch("proto_pool_kernel");
+}
+
+extern "C" int spruce_group_avg_tokens(const void* x, const int64_t xs[4], int64_t B, int64_t H, int64_t L,
+                                       int64_t D, int64_t G, int dtype, void* out, void* stream) {
+  ProtoParams p;
+  const int rc = fill_params(p, x, xs, B, H, L, D, G, dtype, out);
+  if (rc) return rc;
+  p.block = 1; p.P = 1; p.nb = 0;
+  if ((D & 7) == 0 && xs[3] == 1) {
+    const int64_t total8 = B * G * L * (D / 8);
+    SPRUCE_REQUIRE((total8 + 255) / 256 < ((int64_t)1 << 31), "tensor too large");
+    hipLaunchKernelGGL(group_avg_kernel, dim3((unsigned)((total8 + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, p, total8);
+  } else {
+    const int64_t total = B * G * L * D;
+    SPRUCE_REQUIRE((total + 255) / 256 < ((int64_t)1 << 31), "tensor too large");
+    hipLaunchKernelGGL(group_avg_scalar_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, p, total);
+  }
+  return check_launch("group_avg_kernel");
+}

@@ -54,6 +54,10 @@ _SIGNATURES = {
         _p, _p, ctypes.c_size_t, _p],
     "spruce_teacher_targets": [
         _p, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _p, _p, _p, _p],
+    "spruce_pack_selected_ids": [_p, ctypes.c_int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
+    "spruce_pack_selected_mask": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
+    "spruce_proto_pool": [_p, _STRIDES, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _p],
+    "spruce_group_avg_tokens": [_p, _STRIDES, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _p],
     "spruce_sparse_prefill_mask": [
         _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _i64,
         _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int, ctypes.c_int,

@@ -9,12 +9,22 @@ heads as the reference passes it, or stay at native KV resolution
 is needed.  Two HIP passes (row statistics, then tile mass) behind the C ABI;
 ``head_chunk`` is accepted for signature compatibility and ignored (nothing
 is materialised per head).
+
+Selector prototype features (teacher/chunked_extract.py:27-80 in the
+reference), in the model dtype: ``_group_avg_tokens(x, G)`` and
+``_proto_pool_seq(x, block, P)`` with the reference's signatures, plus
+``proto_pool_grouped(query, G, block, P)``, which fuses the two (the per-token
+group average never goes to HBM).  Prototype 0 is the mean of the block's
+real rows; prototypes 1..P-1 are the rows farthest from it in float32 squared
+L2 (farthest first, ties to the lower row), and slots past the real rows hold
+the mean.
 """
 import torch
 
 import spruce_hip
 
 _BLOCK = 64
+_PROTO = 8
 
 
 @torch.no_grad()
@@ -45,3 +55,66 @@ def chunked_pool(query, key, scaling, block_size=_BLOCK, head_chunk=None):
             spruce_hip.ptr(mass), spruce_hip.ptr(ws), nbytes, spruce_hip.stream_of(query))
     spruce_hip.check(rc, "spruce_teacher_block_mass")
     return mass
+
+
+def _features_input(x, name):
+    if not x.is_cuda:
+        raise RuntimeError(f"{name} (HIP) requires GPU tensors")
+    if x.dim() != 4:
+        raise ValueError(f"{name} expects [b, H, L, d], got {tuple(x.shape)}")
+
+
+def _launch_proto(x, G, block, P):
+    b, H, L, d = x.shape
+    if H % G:
+        raise ValueError(f"H={H} not divisible by G={G}")
+    if not 1 <= block <= 64:
+        raise ValueError(f"the HIP prototype kernel supports 1 <= block <= 64, got {block}")
+    if d > 128:
+        raise ValueError(f"the HIP prototype kernel supports head_dim <= 128, got {d}")
+    if x.stride(-1) == 1 and d % 8 == 0 and (x.data_ptr() % 16 or any((s * x.element_size()) % 16 for s in x.stride()[:3])):
+        x = x.contiguous()
+    nb = (L + block - 1) // block
+    out = torch.empty((b, G, nb, P, d), device=x.device, dtype=x.dtype)
+    if out.numel() == 0:
+        return out
+    with torch.cuda.device(x.device):
+        rc = spruce_hip.lib().spruce_proto_pool(
+            spruce_hip.ptr(x), spruce_hip.strides(x), b, H, L, d, G, block, P,
+            spruce_hip.dtype_code(x), spruce_hip.ptr(out), spruce_hip.stream_of(x))
+    spruce_hip.check(rc, "spruce_proto_pool")
+    return out
+
+
+@torch.no_grad()
+def _proto_pool_seq(x, block, P):
+    """[b,H,L,d] -> [b,H,nb,P,d]: P prototype vectors per block (mean + P-1 outliers)."""
+    _features_input(x, "_proto_pool_seq")
+    return _launch_proto(x, x.shape[1], block, P)
+
+
+@torch.no_grad()
+def proto_pool_grouped(query, G, block=_BLOCK, P=_PROTO):
+    """_proto_pool_seq(_group_avg_tokens(query, G), block, P) in one kernel: [b,H,L,d] -> [b,G,nb,P,d]."""
+    _features_input(query, "proto_pool_grouped")
+    return _launch_proto(query, G, block, P)
+
+
+@torch.no_grad()
+def _group_avg_tokens(x, G):
+    """[b,H,L,d] -> [b,G,L,d]: the H/G query heads of each KV group averaged per token."""
+    _features_input(x, "_group_avg_tokens")
+    b, H, L, d = x.shape
+    if H % G:
+        raise AssertionError(f"H={H} not divisible by G={G}")
+    if x.stride(-1) == 1 and d % 8 == 0 and (x.data_ptr() % 16 or any((s * x.element_size()) % 16 for s in x.stride()[:3])):
+        x = x.contiguous()
+    out = torch.empty((b, G, L, d), device=x.device, dtype=x.dtype)
+    if out.numel() == 0:
+        return out
+    with torch.cuda.device(x.device):
+        rc = spruce_hip.lib().spruce_group_avg_tokens(
+            spruce_hip.ptr(x), spruce_hip.strides(x), b, H, L, d, G,
+            spruce_hip.dtype_code(x), spruce_hip.ptr(out), spruce_hip.stream_of(x))
+    spruce_hip.check(rc, "spruce_group_avg_tokens")
+    return out

@@ -63,6 +63,23 @@ def test_invalid_arguments_return_einval_with_message(kwargs, message):
     assert message in spruce_hip.last_error()
 
 
+def test_packing_and_proto_validation_before_launch():
+    lib = spruce_hip.lib()
+    fake = ctypes.c_void_p(1 << 20)
+    # k_selected 2 cannot hold local window 2 plus one sink block.
+    assert lib.spruce_pack_selected_ids(fake, 8, 4, 4, 2, 4, 2, 1, 1, fake, 2, None) == -1
+    assert "sink block" in spruce_hip.last_error()
+    # out_cols must equal min(k, C + sink + lw + 1) = min(8, 2 + 0 + 2) = 4.
+    assert lib.spruce_pack_selected_ids(fake, 4, 4, 4, 2, 4, 8, 1, 0, fake, 8, None) == -1
+    assert "4 columns" in spruce_hip.last_error()
+    assert lib.spruce_pack_selected_mask(fake, 4, 4, 4, 1, 1, fake, 1, None) == -1
+    assert "cannot fit local window" in spruce_hip.last_error()
+    assert lib.spruce_proto_pool(fake, _strides(0, 0, 256, 1), 1, 4, 64, 256, 4, 64, 8, 0, fake, None) == -1
+    assert "head_dim must be <= 128" in spruce_hip.last_error()
+    assert lib.spruce_group_avg_tokens(fake, _strides(0, 0, 128, 1), 1, 6, 64, 128, 4, 0, fake, None) == -1
+    assert "not divisible" in spruce_hip.last_error()
+
+
 def test_error_codes_map_to_reference_exception_types():
     assert _call_index(D=96) == -1
     with pytest.raises(ValueError, match="head_dim"):

@@ -1,0 +1,92 @@
+"""Selector prototype features (HIP, through the C ABI) against the oracle.
+
+Bar: bit-exact (same float32 operation order and model-dtype rounding as
+oracle/proto.c).  Cases: the reference's own known answers (needle kept in
+fp32/fp16/bf16, ragged block padded with the mean), query-side group averaging
+(28 query heads over 4 KV groups) and key-side pooling (no averaging), all
+three dtypes, strided query views ([B,T,H,D] storage as the HF hook passes
+it), head_dim 4 (the scalar path), block < 64 and P > block + 1.  Full size
+(the cfg3 shapes, T = 65536): every block of one KV group against the oracle,
+plus mean-prototype invariants over all groups.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle.selector as osel
+from spruce_hip import workloads
+from teacher.chunked_extract import _group_avg_tokens, _proto_pool_seq, proto_pool_grouped
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+_NAMES = {torch.float32: "float32", torch.float16: "float16", torch.bfloat16: "bfloat16"}
+
+
+def _oracle(x, G, block, P):
+    name = _NAMES[x.dtype]
+    a = x.float().cpu().numpy()
+    if G != x.shape[1]:
+        a = osel.group_avg(a, G, name)
+    return osel.proto_pool(a, block, P, name)
+
+
+def _same(got, exp, what):
+    g = got.float().cpu().numpy()
+    bad = np.argwhere(~((g == exp) | (np.isnan(g) & np.isnan(exp))))
+    assert bad.size == 0, (what, bad[:5].tolist(), g[tuple(bad[0])], exp[tuple(bad[0])])
+
+
+def test_reference_known_answers():
+    torch.manual_seed(0)
+    for dtype in (torch.float32, torch.float16, torch.bfloat16):
+        x = (torch.randn(1, 1, 64, 128) * 0.01).to(dtype)
+        x[0, 0, 37, :] = 40.0
+        out = _proto_pool_seq(x.to(DEV), 64, 8).cpu()
+        assert out.dtype == dtype and out.shape == (1, 1, 1, 8, 128)
+        assert torch.equal(out[0, 0, 0, 1], x[0, 0, 37])
+        _same(out, _oracle(x, 1, 64, 8), f"needle {dtype}")
+    x = torch.randn(1, 1, 67, 4)
+    last = _proto_pool_seq(x.to(DEV), 64, 8)[0, 0, 1].cpu()
+    torch.testing.assert_close(last[0], x[0, 0, 64:].mean(dim=0), atol=1e-5, rtol=0)
+    assert not (last == 0).all(dim=-1).any()
+
+
+@pytest.mark.parametrize("dtype,B,H,G,L,d,block,P,layout", [
+    (torch.bfloat16, 1, 28, 4, 1000, 128, 64, 8, "bthd"),
+    (torch.bfloat16, 2, 4, 4, 700, 128, 64, 8, "bhtd"),
+    (torch.float16, 1, 8, 2, 333, 64, 64, 8, "bthd"),
+    (torch.float32, 1, 6, 3, 260, 32, 64, 8, "bhtd"),
+    (torch.bfloat16, 1, 4, 2, 150, 4, 64, 8, "bhtd"),     # head_dim 4: scalar path
+    (torch.float16, 1, 2, 1, 100, 16, 8, 12, "bhtd"),     # block 8, P > block + 1
+])
+def test_proto_pool_matches_oracle(dtype, B, H, G, L, d, block, P, layout):
+    g = torch.Generator().manual_seed(L + H)
+    if layout == "bthd":
+        x = torch.randn(B, L, H, d, generator=g).to(dtype).transpose(1, 2)
+    else:
+        x = torch.randn(B, H, L, d, generator=g).to(dtype)
+    x[:, :, 5] *= 30.0                                   # planted outlier rows
+    xd = x.to(DEV) if layout == "bhtd" else x.transpose(1, 2).contiguous().to(DEV).transpose(1, 2)
+    got = proto_pool_grouped(xd, G, block, P)
+    _same(got, _oracle(x, G, block, P), "grouped")
+    if G != H:
+        avg = _group_avg_tokens(xd, G)
+        _same(avg, osel.group_avg(x.float().numpy(), G, _NAMES[dtype]), "group avg")
+        _same(_proto_pool_seq(avg, block, P), _oracle(x, G, block, P), "two-step")
+
+
+def test_full_size_cfg3_one_group_and_invariants():
+    print("cfg3 protos: generating inputs", flush=True)
+    q, k, _ = workloads.qkv(0, 65536, 28, 4, 128, torch.bfloat16, use_rope=False, layout="bthd")
+    qd = q.transpose(1, 2).contiguous().to(DEV).transpose(1, 2)
+    kd = k.to(DEV)
+    pq = proto_pool_grouped(qd, 4)
+    pk = _proto_pool_seq(kd, 64, 8)
+    torch.cuda.synchronize()
+    assert pq.shape == (1, 4, 1024, 8, 128) and pk.shape == (1, 4, 1024, 8, 128)
+    print("cfg3 protos: oracle for KV group 2", flush=True)
+    _same(pq[:, 2:3], _oracle(q[:, 14:21], 1, 64, 8), "cfg3 q group 2")
+    _same(pk[:, 2:3], _oracle(k[:, 2:3], 1, 64, 8), "cfg3 k group 2")
+    # Mean prototype of every group equals the block mean of the group-averaged tokens.
+    qm = q.float().reshape(1, 4, 7, 1024, 64, 128).mean(dim=(2, 4)).to(DEV)
+    torch.testing.assert_close(pq[:, :, :, 0].float(), qm, atol=2e-2, rtol=1e-2)
