@@ -236,6 +236,27 @@ int spruce_group_avg_tokens(const void* x, const int64_t xs[4], int64_t B, int64
                             int64_t G, int dtype, void* out, void* stream);
 
 /*
+ * Residual-tree K/V summary table.  Replaces build_kv_summary_table
+ * (sparse/summaries.py:52-142): for each of R token ranges [start, end)
+ * (range_starts / range_ends, int64 device arrays, one per tree node and
+ * prototype as _prototype_token_ranges builds them, :29-49), the float32 mean
+ * of the valid K and V rows and the valid-token count.
+ *   k, v        [B, Hkv, T, D] strided (element strides ks, vs).
+ *   valid       uint8 [B, T] key-padding mask (nonzero = real token) or NULL.
+ *   keys/values float32 [B, Hkv, R, D]; counts, log_counts float32 [B, R];
+ *               mean = sum / max(count, 1); log_counts = -inf where count = 0.
+ *   workspace   >= spruce_kv_summary_workspace_bytes(B, Hkv, T, D) bytes,
+ *               256-byte aligned (per-64-token chunk sums).
+ * Range bounds are clamped to [0, T] on the device.
+ */
+size_t spruce_kv_summary_workspace_bytes(int64_t B, int64_t Hkv, int64_t T, int64_t D);
+int spruce_kv_summary(const void* k, const int64_t ks[4], const void* v, const int64_t vs[4], int64_t B,
+                      int64_t Hkv, int64_t T, int64_t D, int dtype, const uint8_t* valid,
+                      const int64_t* range_starts, const int64_t* range_ends, int64_t R, float* keys,
+                      float* values, float* counts, float* log_counts, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/*
  * Packs compact traversal IDs into selected_blocks rows.  Replaces
  * selected_ids_to_blocks (scripts/export_selected_blocks.py:79-175), same
  * policy: forced sink blocks [0, min(sink_blocks, key_blocks)) strictly before

@@ -57,6 +57,9 @@ _SIGNATURES = {
     "spruce_pack_selected_ids": [_p, ctypes.c_int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "spruce_pack_selected_mask": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "spruce_proto_pool": [_p, _STRIDES, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _p],
+    "spruce_kv_summary": [
+        _p, _STRIDES, _p, _STRIDES, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _p, _p, _i64,
+        _p, _p, _p, _p, _p, ctypes.c_size_t, _p],
     "spruce_group_avg_tokens": [_p, _STRIDES, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _p],
     "spruce_sparse_prefill_mask": [
         _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _i64,
@@ -88,6 +91,8 @@ def lib():
         handle.spruce_version.argtypes = []
         handle.spruce_teacher_workspace_bytes.restype = ctypes.c_size_t
         handle.spruce_teacher_workspace_bytes.argtypes = [_i64, _i64, _i64]
+        handle.spruce_kv_summary_workspace_bytes.restype = ctypes.c_size_t
+        handle.spruce_kv_summary_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64]
         _lib = handle
     return _lib
 
