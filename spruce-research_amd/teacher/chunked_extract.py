@@ -20,6 +20,7 @@ L2 (farthest first, ties to the lower row), and slots past the real rows hold
 the mean.
 """
 import torch
+import torch.nn.functional as F
 
 import spruce_hip
 
@@ -118,3 +119,117 @@ def _group_avg_tokens(x, G):
             spruce_hip.dtype_code(x), spruce_hip.ptr(out), spruce_hip.stream_of(x))
     spruce_hip.check(rc, "spruce_group_avg_tokens")
     return out
+
+
+# ---------------------------------------------------------------------------
+# Hugging Face capture hooks (teacher/chunked_extract.py:134-265 in the reference).
+# The attention function computes the teacher mass (HIP chunked_pool at native
+# KV resolution: no repeated K copy) and the selector prototypes (one fused HIP
+# kernel per side), then propagates the layer through torch's fused causal SDPA
+# as the reference does.
+
+# layer_idx -> pooled mass [1, H, qb, kb] (cpu, float32)
+_CAPTURE = {}
+# layer_idx -> (pooledQ [1, G, qb, P, d], pooledK [1, G, kb, P, d]) (cpu, model dtype)
+_CAPTURE_QK = {}
+_REGISTERED = False
+_FEATURES_REGISTERED = False
+
+
+def _repeat_kv(x, n_rep):
+    if n_rep == 1:
+        return x
+    b, h, t, d = x.shape
+    return x[:, :, None].expand(b, h, n_rep, t, d).reshape(b, h * n_rep, t, d)
+
+
+def _propagate(query, key, value, scaling, dropout):
+    n_rep = query.shape[1] // key.shape[1]
+    out = F.scaled_dot_product_attention(
+        query, _repeat_kv(key, n_rep), _repeat_kv(value, n_rep),
+        attn_mask=None, dropout_p=dropout, scale=scaling, is_causal=True)
+    return out.transpose(1, 2).contiguous()
+
+
+def _capture_qk(module, query, key):
+    groups = key.shape[1]
+    pooled_q = proto_pool_grouped(query, groups, _BLOCK, _PROTO).cpu()
+    pooled_k = _proto_pool_seq(key, _BLOCK, _PROTO).cpu()
+    _CAPTURE_QK[module.layer_idx] = (pooled_q, pooled_k)
+
+
+def _capture_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0,
+                       sliding_window=None, **kwargs):
+    """Attention function "chunked_capture": records mass and prototypes for the layer."""
+    if scaling is None:
+        scaling = query.shape[-1] ** -0.5
+    _CAPTURE[module.layer_idx] = chunked_pool(query, key, scaling, _BLOCK).cpu()
+    _capture_qk(module, query, key)
+    return _propagate(query, key, value, scaling, dropout), None
+
+
+def _capture_features(module, query, key, value, attention_mask, scaling=None, dropout=0.0,
+                      sliding_window=None, **kwargs):
+    """Attention function "selector_feature_capture": prototypes only, no teacher mass."""
+    if scaling is None:
+        scaling = query.shape[-1] ** -0.5
+    _capture_qk(module, query, key)
+    return _propagate(query, key, value, scaling, dropout), None
+
+
+def _ensure_registered():
+    global _REGISTERED
+    if not _REGISTERED:
+        from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+        ALL_ATTENTION_FUNCTIONS.register("chunked_capture", _capture_attention)
+        _REGISTERED = True
+
+
+def _ensure_features_registered():
+    global _FEATURES_REGISTERED
+    if not _FEATURES_REGISTERED:
+        from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+        ALL_ATTENTION_FUNCTIONS.register("selector_feature_capture", _capture_features)
+        _FEATURES_REGISTERED = True
+
+
+def _stack_and_clear_captures(order):
+    """Stack one prompt's per-layer captures along a layer axis, then drop them."""
+    try:
+        return (torch.stack([_CAPTURE[i] for i in order], dim=1),
+                torch.stack([_CAPTURE_QK[i][0] for i in order], dim=1),
+                torch.stack([_CAPTURE_QK[i][1] for i in order], dim=1))
+    finally:
+        _CAPTURE.clear()
+        _CAPTURE_QK.clear()
+
+
+def _set_attn_impl(model, name):
+    model.config._attn_implementation = name
+    for m in model.modules():
+        cfg = getattr(m, "config", None)
+        if cfg is not None:
+            cfg._attn_implementation = name
+
+
+@torch.no_grad()
+def get_pooled_targets(model, tok, prompt, device="cuda", block_size=_BLOCK):
+    """One forward of the base decoder capturing, per layer, the pooled teacher mass and
+    the selector prototypes.  Returns (pooled [1, L, H, qb, kb] float32 cpu,
+    pooledQ [1, L, G, qb, P, d] and pooledK [1, L, G, kb, P, d] in the model dtype on
+    cpu, seq_len)."""
+    if block_size != _BLOCK:
+        raise ValueError("the HIP teacher kernels use block_size=64")
+    _ensure_registered()
+    _CAPTURE.clear()
+    _CAPTURE_QK.clear()
+    prev = model.config._attn_implementation
+    _set_attn_impl(model, "chunked_capture")
+    try:
+        inputs = tok(prompt, return_tensors="pt").to(device)
+        model.model(**inputs, use_cache=False)
+    finally:
+        _set_attn_impl(model, prev)
+    seq_len = inputs["input_ids"].shape[1]
+    pooled, pooled_q, pooled_k = _stack_and_clear_captures(sorted(_CAPTURE))
+    return pooled, pooled_q, pooled_k, seq_len
