@@ -288,7 +288,8 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
 
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * BUF];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps per-wave addresses scalar
   const int l32 = lane & 31, hl = lane >> 5;
 
   // ---- work item.  Workgroups go round-robin to the 8 XCDs (blockIdx % 8);
@@ -417,19 +418,20 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     // S^T (64 keys x 32 queries) as two 32x32 tiles, LDS reads one k-step ahead.
     f32x16_t s0 = f32x16_t{}, s1 = f32x16_t{};
     const uint16_t* kp = Ks + l32 * KSTR + 8 * hl;
-    uint4 a0 = *reinterpret_cast<const uint4*>(kp);
-    uint4 a1 = *reinterpret_cast<const uint4*>(kp + 32 * KSTR);
+    // All K fragments of the block are read before the first MFMA (pinned by
+    // the scheduling barrier), so the matrix cores never wait on a just-issued
+    // LDS read.
+    uint4 a0[KS], a1[KS];
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
-      uint4 n0 = a0, n1 = a1;
-      if (kk + 1 < KS) {
-        n0 = *reinterpret_cast<const uint4*>(kp + 16 * (kk + 1));
-        n1 = *reinterpret_cast<const uint4*>(kp + 32 * KSTR + 16 * (kk + 1));
-      }
-      s0 = mfma32x32x16<F16>(a0, qf[kk], s0);
-      s1 = mfma32x32x16<F16>(a1, qf[kk], s1);
-      a0 = n0;
-      a1 = n1;
+      a0[kk] = *reinterpret_cast<const uint4*>(kp + 16 * kk);
+      a1[kk] = *reinterpret_cast<const uint4*>(kp + 32 * KSTR + 16 * kk);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      s0 = mfma32x32x16<F16>(a0[kk], qf[kk], s0);
+      s1 = mfma32x32x16<F16>(a1[kk], qf[kk], s1);
     }
     if (diag) {
       // Register r of key tile c holds key 32c + 8(r/4) + 4(lane/32) + r%4.
@@ -479,18 +481,20 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     }
     l_run += psum;
     // O^T += V^T P^T, V^T fragments one step ahead.
+    // Same for the V^T fragments; consecutive MFMAs go to different output
+    // tiles (dt fastest), so no MFMA waits on the previous one's result.
     const uint16_t* vp = Vt + l32 * VSTR + 8 * hl;
-    uint4 va = *reinterpret_cast<const uint4*>(vp);
+    uint4 va[DT * 4];
 #pragma unroll
     for (int i = 0; i < DT * 4; ++i) {
-      const int dt = i >> 2, c = (i >> 1) & 1, h2 = i & 1;
-      uint4 vn = va;
-      if (i + 1 < DT * 4) {
-        const int dn = (i + 1) >> 2, cn = ((i + 1) >> 1) & 1, hn = (i + 1) & 1;
-        vn = *reinterpret_cast<const uint4*>(vp + dn * 32 * VSTR + 32 * cn + 16 * hn);
-      }
-      acc[dt] = mfma32x32x16<F16>(va, pk[c][h2], acc[dt]);
-      va = vn;
+      const int dt = i % DT, ch = i / DT, c = ch >> 1, h2 = ch & 1;
+      va[i] = *reinterpret_cast<const uint4*>(vp + dt * 32 * VSTR + 32 * c + 16 * h2);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < DT * 4; ++i) {
+      const int dt = i % DT, ch = i / DT, c = ch >> 1, h2 = ch & 1;
+      acc[dt] = mfma32x32x16<F16>(va[i], pk[c][h2], acc[dt]);
     }
   };
 
