@@ -153,21 +153,81 @@ __global__ __launch_bounds__(256) void block_pool_kernel(const PoolParams p) {
   }
 }
 
-// out[n][j] = fmaf chain over d of x[n][d] * w[d][j]; one thread per output.
+// out[n][j] = fmaf chain over d (in order, from 0) of x[n][d] * w[d][j].
+// A workgroup computes a 32 x 64 output tile, each thread a 2 x 4 register
+// tile; x and w are staged through LDS in 128-wide slices of d (one slice for
+// head_dim <= 128), so there is one load round trip per slice.
+constexpr int kPR = 32, kPC = 64, kPD = 128;
 __global__ __launch_bounds__(256) void project_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                       int64_t N, int D, int P, float* __restrict__ out) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= N * P) return;
-  const int64_t n = idx / P;
-  const int j = (int)(idx - n * P);
-  const float* xr = x + n * D;
-  float acc = 0.f;
-  for (int d = 0; d < D; ++d) acc = __builtin_fmaf(xr[d], w[(int64_t)d * P + j], acc);
-  out[idx] = acc;
+  __shared__ float xs[kPR][kPD + 1];
+  __shared__ __attribute__((aligned(16))) float ws[kPD][kPC];
+  const int tid = threadIdx.x;
+  const int tr = tid >> 4, tc = tid & 15;
+  const int64_t n0 = (int64_t)blockIdx.x * kPR;
+  const int j0 = blockIdx.y * kPC;
+  float acc[2][4];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[a][c] = 0.f;
+  for (int d0 = 0; d0 < D; d0 += kPD) {
+    const int dn = D - d0 < kPD ? D - d0 : kPD;
+    // All loads of the slice are issued before any LDS store (one round trip).
+    float xv_[kPR * kPD / 256], wv_[kPD * kPC / 256];
+#pragma unroll
+    for (int t = 0; t < kPR * kPD / 256; ++t) {
+      const int e = tid + 256 * t, r = e / kPD, dd = e % kPD;
+      const int64_t n = n0 + r;
+      xv_[t] = (n < N && dd < dn) ? x[n * D + d0 + dd] : 0.f;
+    }
+#pragma unroll
+    for (int t = 0; t < kPD * kPC / 256; ++t) {
+      const int e = tid + 256 * t, dd = e / kPC, jj = e % kPC;
+      wv_[t] = (dd < dn && j0 + jj < P) ? w[(int64_t)(d0 + dd) * P + j0 + jj] : 0.f;
+    }
+#pragma unroll
+    for (int t = 0; t < kPR * kPD / 256; ++t) {
+      const int e = tid + 256 * t;
+      xs[e / kPD][e % kPD] = xv_[t];
+    }
+#pragma unroll
+    for (int t = 0; t < kPD * kPC / 256; ++t) {
+      const int e = tid + 256 * t;
+      ws[e / kPC][e % kPC] = wv_[t];
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (int dd = 0; dd < dn; ++dd) {
+      const float4 wv = *reinterpret_cast<const float4*>(&ws[dd][4 * tc]);
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const float xv = xs[2 * tr + a][dd];
+        acc[a][0] = __builtin_fmaf(xv, wv.x, acc[a][0]);
+        acc[a][1] = __builtin_fmaf(xv, wv.y, acc[a][1]);
+        acc[a][2] = __builtin_fmaf(xv, wv.z, acc[a][2]);
+        acc[a][3] = __builtin_fmaf(xv, wv.w, acc[a][3]);
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int a = 0; a < 2; ++a) {
+    const int64_t n = n0 + 2 * tr + a;
+    if (n >= N) continue;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int j = j0 + 4 * tc + c;
+      if (j < P) out[n * P + j] = acc[a][c];
+    }
+  }
 }
 
-// MaxSim scores over a tile of 16 query blocks x 64 key blocks.
-constexpr int kTI = 16, kTJ = 64;
+// MaxSim scores over a tile of 16 query blocks x 64 key blocks: lane = key
+// block, wave = 4 query blocks (their prototype rows are LDS broadcasts).
+// Each score is the fmaf chain over e (in order, from 0) of q . k, maximised
+// over prototype pairs (a outer, c inner, strict >), then divided by div.
+constexpr int kTI = 16, kTJ = 64, kRowsPerWave = kTI / 4;
 struct ScoreParams {
   const float* qp;  // [BG, Qb, Pq, P]
   const float* kp;  // [BG, Kb, Pk, P]
@@ -176,6 +236,25 @@ struct ScoreParams {
   float div;
   int causal;  // 1: j > i is -inf and not computed
 };
+
+// Copies n float4 from src to LDS dst (dst index = map(e)), 8 loads in flight
+// per thread before their stores.
+template <typename Map>
+__device__ __forceinline__ void stage_f4(const float4* __restrict__ src, int n, int valid, Map map) {
+  for (int base = threadIdx.x; base < n; base += 256 * 8) {
+    float4 v[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int e = base + 256 * t;
+      v[t] = e < valid ? src[e] : float4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int e = base + 256 * t;
+      if (e < n) *map(e) = v[t];
+    }
+  }
+}
 
 __global__ __launch_bounds__(256) void gate_scores_kernel(const ScoreParams p) {
   extern __shared__ float lds[];
@@ -188,8 +267,8 @@ __global__ __launch_bounds__(256) void gate_scores_kernel(const ScoreParams p) {
   float* out = p.scores + (int64_t)bg * p.Qb * p.Kb;
   if (p.causal && j0 > i0 + kTI - 1) {
     // Entirely above the diagonal.
-    for (int r = 0; r < 4; ++r) {
-      const int i = i0 + ig * 4 + r;
+    for (int r = 0; r < kRowsPerWave; ++r) {
+      const int i = i0 + ig * kRowsPerWave + r;
       if (i < p.Qb && j < p.Kb) out[(int64_t)i * p.Kb + j] = -INFINITY;
     }
     return;
@@ -197,28 +276,36 @@ __global__ __launch_bounds__(256) void gate_scores_kernel(const ScoreParams p) {
   float* qs = lds;                          // [kTI][Pq*P]
   float* ks = lds + kTI * p.Pq * p.P;       // [kTJ][krow]
   const int qrow = p.Pq * p.P;
-  for (int e = tid; e < kTI * qrow; e += 256) {
-    const int r = e / qrow, off = e - r * qrow;
-    const int i = i0 + r;
-    qs[e] = i < p.Qb ? p.qp[((int64_t)bg * p.Qb + i) * qrow + off] : 0.f;
+  {
+    const int rows = p.Qb - i0 < kTI ? p.Qb - i0 : kTI;
+    const float4* src = reinterpret_cast<const float4*>(p.qp + ((int64_t)bg * p.Qb + i0) * qrow);
+    float4* dst = reinterpret_cast<float4*>(qs);
+    stage_f4(src, kTI * qrow / 4, rows * qrow / 4, [&](int e) { return dst + e; });
   }
-  const int kr = p.Pk * p.P;
-  for (int e = tid; e < kTJ * kr; e += 256) {
-    const int r = e / kr, off = e - r * kr;
-    const int jj = j0 + r;
-    ks[r * krow + off] = jj < p.Kb ? p.kp[((int64_t)bg * p.Kb + jj) * kr + off] : 0.f;
+  const int kr = p.Pk * p.P, kr4 = kr / 4;
+  {
+    const int rows = p.Kb - j0 < kTJ ? p.Kb - j0 : kTJ;
+    const float4* src = reinterpret_cast<const float4*>(p.kp + ((int64_t)bg * p.Kb + j0) * kr);
+    stage_f4(src, kTJ * kr4, rows * kr4, [&](int e) {
+      const int r = e / kr4;
+      return reinterpret_cast<float4*>(ks + r * krow + 4 * (e - r * kr4));
+    });
   }
   __syncthreads();
-  float best[4];
+  const float* qw = qs + ig * kRowsPerWave * qrow;
+  float best[kRowsPerWave];
   for (int a = 0; a < p.Pq; ++a)
     for (int c = 0; c < p.Pk; ++c) {
-      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      float acc[kRowsPerWave];
+#pragma unroll
+      for (int r = 0; r < kRowsPerWave; ++r) acc[r] = 0.f;
       const float* kv = ks + jl * krow + c * p.P;
+#pragma unroll 8
       for (int e = 0; e < p.P; e += 4) {
         const float4 y = *reinterpret_cast<const float4*>(kv + e);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float4 x = *reinterpret_cast<const float4*>(qs + (ig * 4 + r) * qrow + a * p.P + e);
+        for (int r = 0; r < kRowsPerWave; ++r) {
+          const float4 x = *reinterpret_cast<const float4*>(qw + r * qrow + a * p.P + e);
           acc[r] = __builtin_fmaf(x.x, y.x, acc[r]);
           acc[r] = __builtin_fmaf(x.y, y.y, acc[r]);
           acc[r] = __builtin_fmaf(x.z, y.z, acc[r]);
@@ -226,10 +313,11 @@ __global__ __launch_bounds__(256) void gate_scores_kernel(const ScoreParams p) {
         }
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) best[r] = (a == 0 && c == 0) ? acc[r] : (acc[r] > best[r] ? acc[r] : best[r]);
+      for (int r = 0; r < kRowsPerWave; ++r)
+        best[r] = (a == 0 && c == 0) ? acc[r] : (acc[r] > best[r] ? acc[r] : best[r]);
     }
-  for (int r = 0; r < 4; ++r) {
-    const int i = i0 + ig * 4 + r;
+  for (int r = 0; r < kRowsPerWave; ++r) {
+    const int i = i0 + ig * kRowsPerWave + r;
     if (i < p.Qb && j < p.Kb) out[(int64_t)i * p.Kb + j] = (!p.causal || j <= i) ? best[r] / p.div : -INFINITY;
   }
 }
@@ -301,6 +389,62 @@ __global__ __launch_bounds__(256) void causal_topk_kernel(const float* __restric
   }
 }
 
+// Causal top-k with one wavefront per row (rows up to kWaveTopkKb keys): each
+// lane holds keys j = lane + 64 s in registers.  A 32-step binary search over
+// order keys finds the k-th largest key T (the largest T with at least k keys
+// >= T), counting with ballots; then an in-order compaction takes every key
+// above T and the lowest-index keys equal to it.  Same result as
+// causal_topk_kernel, without LDS atomics or a serial bin scan.
+constexpr int kWaveTopkKb = 1024;
+constexpr int kWaveTopkPer = kWaveTopkKb / 64;
+__global__ __launch_bounds__(256) void causal_topk_wave_kernel(const float* __restrict__ scores, int64_t rows,
+                                                               int Qb, int Kb, int k, int32_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // whole wavefront; no block barrier follows
+  const int i = (int)(row % Qb);
+  const int n = i + 1 < Kb ? i + 1 : Kb;
+  int32_t* o = out + row * k;
+  if (n <= k) {
+    for (int t = lane; t < k; t += 64) o[t] = t < n ? t : -1;
+    return;
+  }
+  const float* srow = scores + row * Kb;
+  uint32_t key[kWaveTopkPer];
+#pragma unroll
+  for (int s = 0; s < kWaveTopkPer; ++s) {
+    const int j = lane + 64 * s;
+    key[s] = j < n ? order_key(srow[j] + 0.0f) : 0u;  // -0 -> +0; absent keys rank below all
+  }
+  uint32_t T = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = T | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int s = 0; s < kWaveTopkPer; ++s) cnt += __popcll(__ballot(key[s] >= cand));
+    if (cnt >= k) T = cand;
+  }
+  int gt = 0;
+#pragma unroll
+  for (int s = 0; s < kWaveTopkPer; ++s) gt += __popcll(__ballot(key[s] > T));
+  const int rem = k - gt;
+  const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  int eq_base = 0, out_base = 0;
+#pragma unroll
+  for (int s = 0; s < kWaveTopkPer; ++s) {
+    const int j = lane + 64 * s;
+    const bool valid = j < n;
+    const bool eq = valid && key[s] == T;
+    const uint64_t eqb = __ballot(eq);
+    const int rank = eq_base + __popcll(eqb & lt);
+    const bool sel = valid && (key[s] > T || (eq && rank < rem));
+    const uint64_t sb = __ballot(sel);
+    if (sel) o[out_base + __popcll(sb & lt)] = j;
+    eq_base += __popcll(eqb);
+    out_base += __popcll(sb);
+  }
+}
+
 }  // namespace spruce
 
 using namespace spruce;
@@ -348,10 +492,11 @@ extern "C" int spruce_gate_project(const float* x, const float* w, int64_t N, in
                                    void* stream) {
   SPRUCE_REQUIRE(x && w && out, "x, w and out must be non-null");
   SPRUCE_REQUIRE(N >= 1 && D >= 1 && P >= 1 && N * P < ((int64_t)1 << 40), "invalid projection shape");
-  const int64_t blocks = (N * P + 255) / 256;
-  SPRUCE_REQUIRE(blocks < ((int64_t)1 << 31), "projection too large");
-  hipLaunchKernelGGL(project_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, x, w, N, (int)D,
-                     (int)P, out);
+  const int64_t rows = (N + kPR - 1) / kPR;
+  SPRUCE_REQUIRE(rows < ((int64_t)1 << 31) && P < ((int64_t)1 << 20) && D < ((int64_t)1 << 20),
+                 "projection too large");
+  hipLaunchKernelGGL(project_kernel, dim3((unsigned)rows, (unsigned)((P + kPC - 1) / kPC)), dim3(256), 0,
+                     (hipStream_t)stream, x, w, N, (int)D, (int)P, out);
   return check_launch("project_kernel");
 }
 
@@ -383,6 +528,12 @@ extern "C" int spruce_causal_topk(const float* scores, int64_t R, int64_t Qb, in
   SPRUCE_REQUIRE(Kb <= kTopkMaxKb, "at most %d key blocks per row are supported, got %lld", kTopkMaxKb,
                  (long long)Kb);
   SPRUCE_REQUIRE(R * Qb < ((int64_t)1 << 31), "too many rows");
+  if (Kb <= kWaveTopkKb) {
+    const int64_t rows = R * Qb;
+    hipLaunchKernelGGL(causal_topk_wave_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                       (hipStream_t)stream, scores, rows, (int)Qb, (int)Kb, (int)k, out);
+    return check_launch("causal_topk_wave_kernel");
+  }
   hipLaunchKernelGGL(causal_topk_kernel, dim3((unsigned)(R * Qb)), dim3(256), 0, (hipStream_t)stream, scores,
                      (int)Qb, (int)Kb, (int)k, out);
   return check_launch("causal_topk_kernel");
