@@ -322,6 +322,41 @@ __global__ __launch_bounds__(256) void gate_scores_kernel(const ScoreParams p) {
   }
 }
 
+// The same scores for prototype counts whose tiles do not fit in LDS (e.g.
+// 8 x 8 prototypes of 128 dims): one thread per score, operands read through
+// the cache, identical operation order.
+__global__ __launch_bounds__(256) void gate_scores_direct_kernel(const ScoreParams p, int64_t total) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= total) return;
+  const int j = (int)(idx % p.Kb);
+  const int64_t r = idx / p.Kb;
+  const int i = (int)(r % p.Qb);
+  const int64_t bg = r / p.Qb;
+  float v = -INFINITY;
+  if (!p.causal || j <= i) {
+    const float* qrow = p.qp + (bg * p.Qb + i) * (int64_t)p.Pq * p.P;
+    const float* krow = p.kp + (bg * p.Kb + j) * (int64_t)p.Pk * p.P;
+    float best = 0.f;
+    for (int a = 0; a < p.Pq; ++a)
+      for (int c = 0; c < p.Pk; ++c) {
+        const float4* x = reinterpret_cast<const float4*>(qrow + a * p.P);
+        const float4* y = reinterpret_cast<const float4*>(krow + c * p.P);
+        float acc = 0.f;
+#pragma unroll 4
+        for (int e = 0; e < p.P / 4; ++e) {
+          const float4 xv = x[e], yv = y[e];
+          acc = __builtin_fmaf(xv.x, yv.x, acc);
+          acc = __builtin_fmaf(xv.y, yv.y, acc);
+          acc = __builtin_fmaf(xv.z, yv.z, acc);
+          acc = __builtin_fmaf(xv.w, yv.w, acc);
+        }
+        best = (a == 0 && c == 0) ? acc : (acc > best ? acc : best);
+      }
+    v = best / p.div;
+  }
+  p.scores[idx] = v;
+}
+
 // Causal top-k per row: radix select (4 passes of 8 bits over order keys) for
 // the k-th largest key, then an in-order compaction that takes every larger key
 // and the lowest-index entries equal to it.  One workgroup per row.
@@ -507,10 +542,18 @@ extern "C" int spruce_gate_scores(const float* qp, const float* kp, int64_t BG, 
   SPRUCE_REQUIRE(P >= 4 && P % 4 == 0, "projection dim must be a positive multiple of 4, got %lld", (long long)P);
   SPRUCE_REQUIRE(reinterpret_cast<uintptr_t>(qp) % 16 == 0 && reinterpret_cast<uintptr_t>(kp) % 16 == 0,
                  "qp and kp must be 16-byte aligned");
-  const int64_t lds = (int64_t)(kTI * Pq * P + kTJ * (Pk * P + 4)) * 4;
-  SPRUCE_REQUIRE(lds <= 160 * 1024, "prototype tiles need %lld bytes of LDS (max 163840)", (long long)lds);
-  SPRUCE_REQUIRE(BG < 65536, "too many (batch, head) slabs");
+  SPRUCE_REQUIRE(BG < 65536 && Qb < (1 << 30) && Kb < (1 << 30) && Pq * Pk * P < ((int64_t)1 << 30),
+                 "score shape out of range");
   ScoreParams p{qp, kp, scores, (int)Qb, (int)Kb, (int)Pq, (int)Pk, (int)P, div, causal ? 1 : 0};
+  const int64_t lds = (int64_t)(kTI * Pq * P + kTJ * (Pk * P + 4)) * 4;
+  if (lds > 160 * 1024) {
+    const int64_t total = BG * Qb * Kb;
+    const int64_t blocks = (total + 255) / 256;
+    SPRUCE_REQUIRE(blocks < ((int64_t)1 << 31), "score matrix too large");
+    hipLaunchKernelGGL(gate_scores_direct_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, p,
+                       total);
+    return check_launch("gate_scores_direct_kernel");
+  }
   const dim3 grid((unsigned)((Qb + kTI - 1) / kTI), (unsigned)((Kb + kTJ - 1) / kTJ), (unsigned)BG);
   if (lds > 64 * 1024) {
     const hipError_t e = hipFuncSetAttribute((const void*)gate_scores_kernel,

@@ -55,6 +55,20 @@ def test_projection_scores_and_topk_are_bit_exact():
     assert np.array_equal(_np(sel), osel.topk(osel.scores(eqp, ekp), 5))
 
 
+def test_scores_with_eight_prototypes_per_side_are_bit_exact():
+    # The reference's captured features carry 8 prototypes per block on each
+    # side; their tiles exceed LDS, so the direct kernel computes them.
+    gen = torch.Generator().manual_seed(13)
+    S, Qb, Pq, Pk, P = 2, 45, 8, 8, 128
+    qp = torch.randn(S, Qb, Pq, P, generator=gen)
+    kp = torch.randn(S, Qb, Pk, P, generator=gen)
+    for causal in (True, False):
+        got = gate_scores(qp.to(DEV), kp.to(DEV), causal=causal)
+        assert np.array_equal(_np(got), osel.scores(qp.numpy(), kp.numpy(), causal=causal)), causal
+    sel = causal_topk_blocks(gate_scores(qp.to(DEV), kp.to(DEV)), 8)
+    assert np.array_equal(_np(sel), osel.topk(osel.scores(qp.numpy(), kp.numpy()), 8))
+
+
 def test_topk_ties_short_rows_and_negative_zero():
     gen = torch.Generator().manual_seed(11)
     s = torch.randn(2, 300, 300, generator=gen)
