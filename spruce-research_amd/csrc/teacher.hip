@@ -49,7 +49,8 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
 
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * KTILE];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps per-wave addresses scalar
   const int l32 = lane & 31, hl = lane >> 5;
 
   const int nrows = p.B * p.Hkv * p.Qb;
