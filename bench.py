@@ -176,8 +176,8 @@ def main():
     if not args.no_extra:
         from selector.select import select_blocks
         T3 = 65536
-        q3, k3, _ = workloads.qkv(args.seed, T3, Hq, Hkv, D, torch.bfloat16, use_rope=False,
-                                  layout="bthd", device="cuda")
+        q3, k3, v3 = workloads.qkv(args.seed, T3, Hq, Hkv, D, torch.bfloat16, use_rope=False,
+                                   layout="bthd", device="cuda")
         Wq, Wk = (w.to(dev) for w in workloads.cfg3_gate_weights(args.seed))
         fn3 = lambda: select_blocks(q3, k3, Wq, Wk, top_k=32)  # noqa: E731
         _, k3ms = _time_launches(fn3, max(10, args.steps // 2), max(3, args.warmup // 2))
@@ -190,7 +190,56 @@ def main():
             "compulsory_bytes": by3, "top_k": 32,
             "stages": "pool (Q group+block mean, K mean/max) -> project -> MaxSim scores -> causal top-k",
         }
-        del q3, k3
+
+        # Selector prototype features of the reference's capture hook: Q
+        # group-averaged and pooled to mean + 7 outliers per block, K likewise.
+        from teacher.chunked_extract import _proto_pool_seq, proto_pool_grouped
+        fnp = lambda: (proto_pool_grouped(q3, Hkv, 64, 8), _proto_pool_seq(k3, 64, 8))  # noqa: E731
+        _, kpms = _time_launches(fnp, max(10, args.steps // 2), max(3, args.warmup // 2))
+        mp = statistics.median(kpms)
+        byp = (Hq + Hkv) * T3 * D * 2 + 2 * Hkv * (T3 // 64) * 8 * D * 2
+        configs["cfg3_proto_features_64k"] = {
+            "ms_median": round(mp, 4), "ms_min": round(min(kpms), 4), "ms_max": round(max(kpms), 4),
+            "gbps": round(byp / (mp * 1e-3) / 1e9, 1),
+            "frac_hbm_peak": round(byp / (mp * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "compulsory_bytes": byp, "prototypes": 8,
+        }
+
+        # Residual-tree K/V summary table (4 positional prototypes per node).
+        from interfaces.residual_summaries import build_residual_tree_layout
+        from sparse.summaries import build_kv_summary_table
+        k3h, v3h = k3.contiguous(), v3.contiguous()
+        lay = build_residual_tree_layout(T3 // 64)
+        fns = lambda: build_kv_summary_table(k3h, v3h, lay, block_size=64, prototypes=4)  # noqa: E731
+        _, ksms = _time_launches(fns, max(10, args.steps // 2), max(3, args.warmup // 2))
+        ms_ = statistics.median(ksms)
+        bys = 2 * Hkv * T3 * D * 2 + 2 * Hkv * lay.num_nodes * 4 * D * 4 + 2 * lay.num_nodes * 4 * 4
+        configs["cfg3_kv_summaries_64k"] = {
+            "ms_median": round(ms_, 4), "ms_min": round(min(ksms), 4), "ms_max": round(max(ksms), 4),
+            "gbps": round(bys / (ms_ * 1e-3) / 1e9, 1),
+            "frac_hbm_peak": round(bys / (ms_ * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "compulsory_bytes": bys, "nodes": lay.num_nodes, "prototypes": 4,
+            "note": "includes building the token-range table on the device each call",
+        }
+        del q3, k3, v3, k3h, v3h
+
+    # ---- route packing at the cfg5 grid: 4 KV heads x 2048 query blocks,
+    # 96 traversal candidates per row into 64-wide selected_blocks rows.
+    if not args.no_extra:
+        from interfaces.packing import selected_ids_to_blocks
+        gen = torch.Generator(device=dev).manual_seed(args.seed)
+        ids6 = torch.randint(0, 2048, (1, Hkv, 2048, 96), generator=gen, device=dev, dtype=torch.int64)
+        fn6 = lambda: selected_ids_to_blocks(ids6, 64, 1, None, 1)  # noqa: E731
+        _, k6ms = _time_launches(fn6, max(10, args.steps // 2), max(3, args.warmup // 2))
+        m6 = statistics.median(k6ms)
+        by6 = ids6.numel() * 8 + Hkv * 2048 * 64 * 4
+        configs["cfg5_route_packing"] = {
+            "ms_median": round(m6, 4), "ms_min": round(min(k6ms), 4), "ms_max": round(max(k6ms), 4),
+            "gbps": round(by6 / (m6 * 1e-3) / 1e9, 1),
+            "frac_hbm_peak": round(by6 / (m6 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "compulsory_bytes": by6, "rows": Hkv * 2048, "candidates": 96, "k_selected": 64,
+        }
+        del ids6
 
     # ---- cfg4: teacher block mass + targets, T=16384 (256 blocks)
     if not args.no_extra:

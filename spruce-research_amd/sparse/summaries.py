@@ -33,11 +33,26 @@ class KVSummaryTable:
     range_ends: torch.Tensor
 
 
+_RANGE_CACHE = {}
+
+
 def _prototype_token_ranges(layout: ResidualTreeLayout, *, seq_len: int, block_size: int,
                             prototypes: int, device) -> tuple[torch.Tensor, torch.Tensor]:
     """Token ranges ``[node, P]``: slice p of node [s, e) is
     ``[s + len * p // P, s + len * (p + 1) // P)`` with the node's token range
-    ``[start * block_size, end * block_size)`` clipped to ``seq_len``."""
+    ``[start * block_size, end * block_size)`` clipped to ``seq_len``.  The
+    tables depend only on the layout and sizes, so they are built once per
+    device and reused (the layout is immutable)."""
+    key = (layout.num_leaves, seq_len, block_size, prototypes, str(device))
+    hit = _RANGE_CACHE.get(key)
+    if hit is not None and hit[0] is layout:
+        return hit[1], hit[2]
+    starts, ends = _build_token_ranges(layout, seq_len, block_size, prototypes, device)
+    _RANGE_CACHE[key] = (layout, starts, ends)
+    return starts, ends
+
+
+def _build_token_ranges(layout, seq_len, block_size, prototypes, device):
     first = (torch.tensor(layout.starts, device=device, dtype=torch.long) * block_size).clamp_max(seq_len)
     last = (torch.tensor(layout.ends, device=device, dtype=torch.long) * block_size).clamp_max(seq_len)
     length = (last - first)[:, None]
