@@ -9,17 +9,17 @@
 //   values[b, h, r]  = the same over V
 //   log_counts[b, r] = log(count), or -inf when the range holds no valid token
 // The reference forms the sums as differences of float32 prefix sums; here
-// they are direct float32 sums (smaller rounding error, same value up to it).
+// they are float32 sums over a dyadic table (pairwise, so the rounding error
+// grows with log2 of the range length rather than with the position in the
+// sequence).
 //
-// chunk_sum: one pass over K and V writing per-64-token chunk sums (and valid
-// counts) to the workspace.  For 16-byte-aligned rows (the usual case) a
-// float64 exclusive prefix of the chunk sums follows, and range_sum adds, per
-// (b, h, range), the prefix difference over the fully covered chunks and the
-// tokens of the partial chunks at either end (16-byte loads, LDS reduction):
-// upper tree levels never re-read K/V and each range costs O(1) chunk reads.
-// Other layouts take a scalar path that adds the covered chunk sums one by
-// one.  HBM-bound: K and V are read about twice (once for the chunk sums,
-// once more for the within-chunk ranges of the two lowest tree levels).
+// Aligned rows (16-byte rows, contiguous last dim, D % 64 == 0, the usual case):
+// pyramid_kernel reads K and V once and builds the dyadic table (16-token
+// leaves, each level the pairwise sums of the one below) in the workspace;
+// range_sum adds, per (b, h, range), the partial leaves at the range ends and
+// the table entries covering the rest: one entry for a tree-node prototype
+// range.  Other layouts take a scalar path: per-64-token chunk sums, then each
+// range adds its covered chunks one by one.  HBM-bound: K and V are read once.
 #include <math.h>
 
 #include "common.h"
@@ -158,219 +158,301 @@ __global__ __launch_bounds__(kSumThreads) void range_sum_kernel(SumParams p) {
   }
 }
 
-// ---------------------------------------------------------------- vector path
-// For 16-byte-aligned rows with a contiguous last dim and D % 8 == 0: thread
-// (r, gc) = (tid / 16, tid % 16) reads 16 bytes (8 columns) of token rows
-// r, r + 16, ... and of granule-columns gc, gc + 16, ... over [K | V]; the 16
-// token lanes are then reduced through LDS.  Full 64-token chunks inside a
-// range come from float64 prefix sums of the chunk sums (two reads per range).
-constexpr int kMaxGranCols = 64;   // 2 * D / 8 for D <= 256
+// ---------------------------------------------------------------- dyadic path
+// For 16-byte-aligned rows with a contiguous last dim and D % 64 == 0 the sums
+// come from a dyadic table over the sequence: level 0 entry i holds the float32
+// sums of tokens [16i, 16i + 16) over all 2D columns of [K | V], and level j
+// entry i = level j-1 entries 2i + 2i+1, i.e. tokens [16 * 2^j * i,
+// 16 * 2^j * (i + 1)).  A range is split into the partial 16-token leaves at
+// its ends and the canonical dyadic cover of the whole leaves between them;
+// a tree-node prototype range (aligned to its own power-of-two size) is a
+// single table entry.  K/V are read once; every range costs one table row.
+constexpr int kLeaf = 16;          // tokens per level-0 entry
+constexpr int kFold = 4;           // levels added per launch: 16 rows -> 1
+constexpr int kMaxLevels = 32;
 
-struct VecParams {
+struct PyrParams {
   SumParams p;
-  double* prefix;     // [B, H, nchunks + 1, 2D] exclusive prefix of chunk sums
-  int* cnt_prefix;    // [B, nchunks + 1]
+  float* pyr;                // [B, H, E, 2D]
+  int* pcnt;                 // [B, E] valid counts (only with a mask)
+  int E;                     // table entries per (b, h)
+  int levels;
+  int off[kMaxLevels];       // first entry of each level
+  int n[kMaxLevels];         // entries of each level
 };
 
-// Adds 8 columns of token t (tensor which, granule gi) into a[0..8).
-__device__ __forceinline__ void add_row8(const SumParams& p, int which, int b, int h, int gi, int64_t t, float* a) {
-  const void* x = which ? p.v : p.k;
-  const int64_t* st = which ? p.vs : p.ks;
-  float v[8];
-  load8f(x, (int64_t)b * st[0] + (int64_t)h * st[1] + t * st[2] + 8 * gi, p.dtype, v);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) a[e] += v[e];
+// Entries per level for T tokens; returns the level count.
+int table_levels(int64_t T, int64_t* n, int64_t* off, int64_t* E) {
+  int L = 0;
+  int64_t m = (T + kLeaf - 1) / kLeaf, o = 0;
+  for (;;) {
+    if (n) n[L] = m;
+    if (off) off[L] = o;
+    o += m;
+    ++L;
+    if (m == 1) break;
+    m = (m + 1) / 2;
+  }
+  if (E) *E = o;
+  return L;
 }
 
-// Sums tokens tok(i), i in [0, n), over all 2D columns into out[0 .. 2D) (LDS).
-template <typename TokOf>
-__device__ __forceinline__ void vec_token_sums(const SumParams& p, int b, int h, int n, TokOf tok, float* red,
-                                               float* out) {
-  const int r = threadIdx.x >> 4, gl = threadIdx.x & 15;
-  const int G = p.D / 8, GC = 2 * G;
-  float acc[kMaxGranCols / 16][8];
+// 8 columns (one 16-byte granule of 16-bit data, two of float32) of a row.
+template <typename In>
+struct Raw8 {
+  uint4 w[In::bytes / 2];
+};
+
+template <typename In>
+__device__ __forceinline__ Raw8<In> ld8(const char* p) {
+  Raw8<In> r;
 #pragma unroll
-  for (int k = 0; k < kMaxGranCols / 16; ++k)
+  for (int i = 0; i < In::bytes / 2; ++i) r.w[i] = reinterpret_cast<const uint4*>(p)[i];
+  return r;
+}
+
+template <typename In>
+__device__ __forceinline__ void add8(const Raw8<In>& r, float* a) {
+  if constexpr (In::code == SPRUCE_DTYPE_F32) {
+    a[0] += __uint_as_float(r.w[0].x); a[1] += __uint_as_float(r.w[0].y);
+    a[2] += __uint_as_float(r.w[0].z); a[3] += __uint_as_float(r.w[0].w);
+    a[4] += __uint_as_float(r.w[1].x); a[5] += __uint_as_float(r.w[1].y);
+    a[6] += __uint_as_float(r.w[1].z); a[7] += __uint_as_float(r.w[1].w);
+  } else {
+    constexpr bool F16 = In::code == SPRUCE_DTYPE_F16;
+    const uint32_t w[4] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[k][e] = 0.f;
-  const uint8_t* valid = p.valid ? p.valid + (int64_t)b * p.T : nullptr;
-  for (int i = r; i < n; i += 16) {
-    const int64_t t = tok(i);
-    if (valid && !valid[t]) continue;
-#pragma unroll
-    for (int k = 0; k < kMaxGranCols / 16; ++k) {
-      const int gc = gl + 16 * k;
-      if (gc < GC) add_row8(p, gc >= G, b, h, gc >= G ? gc - G : gc, t, acc[k]);
+    for (int i = 0; i < 4; ++i) {
+      a[2 * i] += unpack1<F16>(w[i] & 0xffffu);
+      a[2 * i + 1] += unpack1<F16>(w[i] >> 16);
     }
   }
+}
+
+__device__ __forceinline__ void add_f8(const float* src, float* a) {
+  const float4 x = reinterpret_cast<const float4*>(src)[0];
+  const float4 y = reinterpret_cast<const float4*>(src)[1];
+  a[0] += x.x; a[1] += x.y; a[2] += x.z; a[3] += x.w;
+  a[4] += y.x; a[5] += y.y; a[6] += y.z; a[7] += y.w;
+}
+
+// Granule columns of [K | V]: gc in [0, 2D/8), K for gc < D/8.  Lane gl owns
+// gc = gl + 16k, k < NK, with 16 * NK == 2D/8 (D % 64 == 0), so every lane is
+// active for every k.  row[k] points at token 0 of its column, step[k] is the
+// token stride in bytes.
+template <typename In, int NK>
+__device__ __forceinline__ void granule_ptrs(const SumParams& p, int b, int h, int gl, const char** row,
+                                             int64_t* step) {
+  const int G = p.D / 8;
 #pragma unroll
-  for (int k = 0; k < kMaxGranCols / 16; ++k) {
+  for (int k = 0; k < NK; ++k) {
     const int gc = gl + 16 * k;
-    if (gc < GC)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) red[r * 2 * p.D + 8 * gc + e] = acc[k][e];
+    const bool isv = gc >= G;
+    const int64_t* st = isv ? p.vs : p.ks;
+    const char* base = static_cast<const char*>(isv ? p.v : p.k);
+    row[k] = base + ((int64_t)b * st[0] + (int64_t)h * st[1] + 8 * (isv ? gc - G : gc)) * In::bytes;
+    step[k] = st[2] * In::bytes;
   }
-  __syncthreads();
-  for (int col = threadIdx.x; col < 2 * p.D; col += kSumThreads) {
-    float sum = 0.f;
-#pragma unroll
-    for (int rr = 0; rr < 16; ++rr) sum += red[rr * 2 * p.D + col];
-    out[col] = sum;
-  }
-  __syncthreads();
 }
 
-__global__ __launch_bounds__(kSumThreads) void chunk_sum_vec_kernel(SumParams p) {
+// One workgroup per (b, h, segment of 16 entries of level `base`).  With
+// src < 0 the entries are level 0, summed from tokens (thread (r, gl) =
+// (tid / 16, tid % 16) adds the 16 tokens of entry r in order, 16 bytes per
+// granule column) and written; otherwise they are read from level src.  The
+// next kFold levels are then formed by pairwise sums in LDS.
+template <typename In, int NK>
+__global__ __launch_bounds__(kSumThreads) void pyramid_kernel(PyrParams pp, int src) {
   extern __shared__ float lds[];
-  float* red = lds;                  // [16][2D]
-  float* out = lds + 16 * 2 * p.D;   // [2D]
-  const int c = blockIdx.x % p.nchunks;
-  const int bh = blockIdx.x / p.nchunks;
+  const SumParams& p = pp.p;
+  const int W = 2 * p.D;
+  float* buf[2] = {lds, lds + 16 * W};            // [16][W] and [8][W]
+  int* cbuf[2] = {reinterpret_cast<int*>(lds + 24 * W), reinterpret_cast<int*>(lds + 24 * W) + 16};
+  const int base = src < 0 ? 0 : src;
+  const int nbase = pp.n[base];
+  const int nseg = (nbase + 15) / 16;
+  const int seg = blockIdx.x % nseg;
+  const int bh = blockIdx.x / nseg;
   const int h = bh % p.H, b = bh / p.H;
-  const int64_t t0 = (int64_t)c * kChunk;
-  const int n = (int)((t0 + kChunk < p.T ? t0 + kChunk : p.T) - t0);
-  vec_token_sums(p, b, h, n, [&](int i) { return t0 + i; }, red, out);
-  float* dst = p.chunk + (((int64_t)b * p.H + h) * p.nchunks + c) * 2 * p.D;
-  for (int col = threadIdx.x; col < 2 * p.D; col += kSumThreads) dst[col] = out[col];
-  if (h == 0 && threadIdx.x == 0) {
-    int cnt = n;
-    if (p.valid) {
-      cnt = 0;
-      for (int i = 0; i < n; ++i) cnt += p.valid[(int64_t)b * p.T + t0 + i] != 0;
+  const int r = threadIdx.x >> 4, gl = threadIdx.x & 15;
+  const bool counts = pp.pcnt != nullptr && h == 0;
+  float* table = pp.pyr + (int64_t)bh * pp.E * W;
+  const int e = seg * 16 + r;
+  float acc[NK][8];
+#pragma unroll
+  for (int k = 0; k < NK; ++k)
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc[k][q] = 0.f;
+  int cnt = 0;
+  if (e < nbase) {
+    if (src < 0) {
+      const int64_t t0 = (int64_t)e * kLeaf;
+      const int64_t t1 = t0 + kLeaf < p.T ? t0 + kLeaf : p.T;
+      const uint8_t* valid = p.valid ? p.valid + (int64_t)b * p.T : nullptr;
+      const char* row[NK];
+      int64_t step[NK];
+      granule_ptrs<In, NK>(p, b, h, gl, row, step);
+      if (!valid && t1 - t0 == kLeaf) {
+        // All loads of a batch are issued before the first add (about 64
+        // VGPRs of loads in flight per thread); adds stay in token order.
+        constexpr int kBatch = 16 / (NK * (In::bytes / 2)) > 0 ? 16 / (NK * (In::bytes / 2)) : 1;
+        cnt = kLeaf;
+#pragma unroll
+        for (int i0 = 0; i0 < kLeaf; i0 += kBatch) {
+          Raw8<In> raw[kBatch][NK];
+#pragma unroll
+          for (int u = 0; u < kBatch; ++u)
+#pragma unroll
+            for (int k = 0; k < NK; ++k) raw[u][k] = ld8<In>(row[k] + (t0 + i0 + u) * step[k]);
+#pragma unroll
+          for (int u = 0; u < kBatch; ++u)
+#pragma unroll
+            for (int k = 0; k < NK; ++k) add8<In>(raw[u][k], acc[k]);
+        }
+      } else {
+        for (int64_t t = t0; t < t1; ++t) {
+          if (valid && !valid[t]) continue;
+          ++cnt;
+#pragma unroll
+          for (int k = 0; k < NK; ++k) add8<In>(ld8<In>(row[k] + t * step[k]), acc[k]);
+        }
+      }
+      float* out = table + (int64_t)e * W;
+#pragma unroll
+      for (int k = 0; k < NK; ++k) {
+        float4* o = reinterpret_cast<float4*>(out + 8 * (gl + 16 * k));
+        o[0] = make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
+        o[1] = make_float4(acc[k][4], acc[k][5], acc[k][6], acc[k][7]);
+      }
+      if (counts && gl == 0) pp.pcnt[(int64_t)b * pp.E + e] = cnt;
+    } else {
+      const float* row = table + (int64_t)(pp.off[base] + e) * W;
+#pragma unroll
+      for (int k = 0; k < NK; ++k) add_f8(row + 8 * (gl + 16 * k), acc[k]);
+      if (counts) cnt = pp.pcnt[(int64_t)b * pp.E + pp.off[base] + e];
     }
-    p.chunk_cnt[(int64_t)b * p.nchunks + c] = cnt;
   }
-}
-
-// Exclusive float64 prefix over the chunk sums.  A workgroup covers one
-// (b, h) and 16 columns; its 256 threads split the chunks into 16 segments:
-// segment sums, their prefix in LDS, then each segment's running prefix.
-constexpr int kScanCols = 16, kScanSegs = 16;
-__global__ __launch_bounds__(kSumThreads) void chunk_prefix_kernel(VecParams vp) {
-  const SumParams& p = vp.p;
-  __shared__ double segsum[kScanSegs][kScanCols];
-  const int ncg = (2 * p.D + kScanCols - 1) / kScanCols;
-  const int bh = blockIdx.x / ncg, cg = blockIdx.x % ncg;
-  const int b = bh / p.H, h = bh % p.H;
-  const int cl = threadIdx.x % kScanCols, sg = threadIdx.x / kScanCols;
-  const int col = cg * kScanCols + cl;
-  const bool on = col < 2 * p.D;
-  const int per = (p.nchunks + kScanSegs - 1) / kScanSegs;
-  const int c0 = sg * per, c1 = c0 + per < p.nchunks ? c0 + per : p.nchunks;
-  const float* src = p.chunk + (int64_t)bh * p.nchunks * 2 * p.D;
-  double* dst = vp.prefix + (int64_t)bh * (p.nchunks + 1) * 2 * p.D;
-  double sum = 0.0;
-  if (on)
-    for (int c = c0; c < c1; ++c) sum += (double)src[(int64_t)c * 2 * p.D + col];
-  segsum[sg][cl] = sum;
+#pragma unroll
+  for (int k = 0; k < NK; ++k)
+#pragma unroll
+    for (int q = 0; q < 8; ++q) buf[0][r * W + 8 * (gl + 16 * k) + q] = acc[k][q];
+  if (gl == 0) cbuf[0][r] = cnt;
   __syncthreads();
-  double run = 0.0;
-  for (int q = 0; q < sg; ++q) run += segsum[q][cl];
-  if (on) {
-    if (sg == 0) dst[col] = 0.0;
-    for (int c = c0; c < c1; ++c) {
-      run += (double)src[(int64_t)c * 2 * p.D + col];
-      dst[(int64_t)(c + 1) * 2 * p.D + col] = run;
+  for (int f = 1; f <= kFold; ++f) {
+    const int L = base + f;
+    if (L >= pp.levels) break;                      // uniform
+    const float* in = buf[(f - 1) & 1];
+    float* out = buf[f & 1];
+    const int m = 16 >> f;
+    const int first = seg * m;
+    float* dst = table + (int64_t)(pp.off[L] + first) * W;
+    for (int idx = threadIdx.x; idx < m * W; idx += kSumThreads) {
+      const int i = idx / W, col = idx - i * W;
+      const float v = in[2 * i * W + col] + in[(2 * i + 1) * W + col];
+      out[idx] = v;
+      if (first + i < pp.n[L]) dst[idx] = v;
     }
-  }
-  // Valid-token count prefix (only read when a padding mask is given): one
-  // workgroup per batch row, 256 segments of chunks, same three steps.
-  if (p.valid && h == 0 && cg == 0) {
-    __shared__ int cseg[kSumThreads];
-    const int cper = (p.nchunks + kSumThreads - 1) / kSumThreads;
-    const int d0 = threadIdx.x * cper, d1 = d0 + cper < p.nchunks ? d0 + cper : p.nchunks;
-    const int* cc = p.chunk_cnt + (int64_t)b * p.nchunks;
-    int* cp = vp.cnt_prefix + (int64_t)b * (p.nchunks + 1);
-    int seg = 0;
-    for (int c = d0; c < d1; ++c) seg += cc[c];
-    cseg[threadIdx.x] = seg;
+    if (counts && (int)threadIdx.x < m) {
+      const int c = cbuf[(f - 1) & 1][2 * threadIdx.x] + cbuf[(f - 1) & 1][2 * threadIdx.x + 1];
+      cbuf[f & 1][threadIdx.x] = c;
+      if (first + (int)threadIdx.x < pp.n[L]) pp.pcnt[(int64_t)b * pp.E + pp.off[L] + first + threadIdx.x] = c;
+    }
     __syncthreads();
-    int acc = 0;
-    for (int q = 0; q < (int)threadIdx.x; ++q) acc += cseg[q];
-    if (threadIdx.x == 0) cp[0] = 0;
-    for (int c = d0; c < d1; ++c) {
-      acc += cc[c];
-      cp[c + 1] = acc;
-    }
   }
 }
 
-// One wavefront per (b, h, range): lane = (token lane r = lane / 16, granule
-// lane gl = lane % 16); the 4 token lanes are combined with cross-lane
-// shuffles, so the kernel uses no LDS and no barriers.
-__global__ __launch_bounds__(kSumThreads) void range_sum_vec_kernel(VecParams vp) {
-  const SumParams& p = vp.p;
+// One wavefront per (b, h, range): lane = (token lane tl = lane / 16, granule
+// lane gl = lane % 16).  Edge tokens and cover entries are dealt round-robin
+// to the 4 token lanes, which are then combined with cross-lane shuffles (no
+// LDS, no barriers).
+template <typename In, int NK>
+__global__ __launch_bounds__(kSumThreads) void range_pyr_kernel(PyrParams pp) {
+  const SumParams& p = pp.p;
   const int lane = threadIdx.x & 63;
   const int64_t idx = (int64_t)blockIdx.x * (kSumThreads / 64) + (threadIdx.x >> 6);
   if (idx >= (int64_t)p.B * p.H * p.R) return;  // whole wavefront
   const int r = (int)(idx % p.R);
   const int bh = (int)(idx / p.R);
   const int h = bh % p.H, b = bh / p.H;
+  // Ranges come from caller memory: clamp them to [0, T] so a bad table can
+  // only produce wrong sums, never an out-of-bounds read.
   int64_t s = p.starts[r], e = p.ends[r];
   s = s < 0 ? 0 : (s > p.T ? p.T : s);
   e = e < s ? s : (e > p.T ? p.T : e);
-  int64_t c0 = (s + kChunk - 1) / kChunk, c1 = e / kChunk;
-  int64_t head_end = c0 * kChunk, tail_start = c1 * kChunk;
+  // Whole leaves [c0, c1); the last leaf may be short (tokens past T do not
+  // exist), so a range ending at T takes it whole.
+  const int64_t epad = e == p.T ? (int64_t)pp.n[0] * kLeaf : e;
+  int64_t c0 = (s + kLeaf - 1) / kLeaf, c1 = epad / kLeaf;
+  int64_t head_end = c0 * kLeaf, tail_start = c1 * kLeaf;
   if (c1 <= c0) {
     c0 = c1 = 0;
     head_end = e;
     tail_start = e;
   }
-  const int nh = (int)(head_end - s), nt = (int)(e - tail_start);
+  const int nh = (int)(head_end - s), nt = (int)(e > tail_start ? e - tail_start : 0);
   const int tl = lane >> 4, gl = lane & 15;
-  const int G = p.D / 8, GC = 2 * G;
-  constexpr int KG = kMaxGranCols / 16;
-  float acc[KG][8];
+  const int W = 2 * p.D;
+  float acc[NK][8];
 #pragma unroll
-  for (int k = 0; k < KG; ++k)
+  for (int k = 0; k < NK; ++k)
 #pragma unroll
     for (int q = 0; q < 8; ++q) acc[k][q] = 0.f;
   const uint8_t* valid = p.valid ? p.valid + (int64_t)b * p.T : nullptr;
   int nvalid = 0;
-  for (int i = tl; i < nh + nt; i += 4) {
-    const int64_t t = i < nh ? s + i : tail_start + (i - nh);
-    if (valid && !valid[t]) continue;
-    ++nvalid;
+  if (nh + nt > 0) {
+    const char* row[NK];
+    int64_t step[NK];
+    granule_ptrs<In, NK>(p, b, h, gl, row, step);
+    for (int i = tl; i < nh + nt; i += 4) {
+      const int64_t t = i < nh ? s + i : tail_start + (i - nh);
+      if (valid && !valid[t]) continue;
+      ++nvalid;
 #pragma unroll
-    for (int k = 0; k < KG; ++k) {
-      const int gc = gl + 16 * k;
-      if (gc < GC) add_row8(p, gc >= G, b, h, gc >= G ? gc - G : gc, t, acc[k]);
+      for (int k = 0; k < NK; ++k) add8<In>(ld8<In>(row[k] + t * step[k]), acc[k]);
     }
   }
+  const float* table = pp.pyr + (int64_t)bh * pp.E * W;
+  int q = 0;
+  for (int64_t c = c0; c < c1; ++q) {
+    // Largest aligned power-of-two block of leaves starting at c inside [c, c1).
+    int j = 63 - __builtin_clzll((unsigned long long)(c1 - c));
+    if (c != 0) {
+      const int a = __builtin_ctzll((unsigned long long)c);
+      j = a < j ? a : j;
+    }
+    if ((q & 3) == tl) {
+      const int64_t ent = pp.off[j] + (c >> j);
 #pragma unroll
-  for (int k = 0; k < KG; ++k)
+      for (int k = 0; k < NK; ++k) add_f8(table + ent * W + 8 * (gl + 16 * k), acc[k]);
+      if (valid) nvalid += pp.pcnt[(int64_t)b * pp.E + ent];
+    }
+    c += (int64_t)1 << j;
+  }
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      acc[k][q] += __shfl_xor(acc[k][q], 16, 64);
-      acc[k][q] += __shfl_xor(acc[k][q], 32, 64);
+  for (int k = 0; k < NK; ++k)
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      acc[k][u] += __shfl_xor(acc[k][u], 16, 64);
+      acc[k][u] += __shfl_xor(acc[k][u], 32, 64);
     }
   int count = (int)(e - s);
   if (valid) {
-    // nvalid counts each token once per granule lane group: take lane gl = 0's.
+    // Every granule lane of a token lane holds the same count: take gl = 0's.
     int n = gl == 0 ? nvalid : 0;
     n += __shfl_xor(n, 16, 64);
     n += __shfl_xor(n, 32, 64);
-    n = __shfl(n, 0, 64);
-    const int* cp = vp.cnt_prefix + (int64_t)b * (p.nchunks + 1);
-    count = n + (c1 > c0 ? cp[c1] - cp[c0] : 0);
+    count = __shfl(n, 0, 64);
   }
   const float denom = count > 1 ? (float)count : 1.0f;
-  const double* pre = vp.prefix + (int64_t)bh * (p.nchunks + 1) * 2 * p.D;
   const int64_t orow = (((int64_t)b * p.H + h) * p.R + r) * p.D;
   if (tl == 0) {
+    const int G = p.D / 8;
 #pragma unroll
-    for (int k = 0; k < KG; ++k) {
+    for (int k = 0; k < NK; ++k) {
       const int gc = gl + 16 * k;
-      if (gc >= GC) continue;
       const int which = gc >= G, d0 = 8 * (which ? gc - G : gc);
       float* o = (which ? p.values : p.keys) + orow + d0;
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        float v = acc[k][q];
-        const int col = 8 * gc + q;
-        if (c1 > c0) v += (float)(pre[c1 * 2 * p.D + col] - pre[c0 * 2 * p.D + col]);
-        o[q] = v / denom;
-      }
+      for (int u = 0; u < 8; ++u) o[u] = acc[k][u] / denom;
     }
   }
   if (h == 0 && lane == 0) {
@@ -379,14 +461,39 @@ __global__ __launch_bounds__(kSumThreads) void range_sum_vec_kernel(VecParams vp
   }
 }
 
+template <typename In, int NK>
+int launch_dyadic(const PyrParams& pp, int64_t g2, hipStream_t stream) {
+  const size_t lds = (size_t)(24 * 2 * pp.p.D) * sizeof(float) + 32 * sizeof(int);
+  for (int src = -1; src < pp.levels - 1; src = src < 0 ? kFold : src + kFold) {
+    const int64_t nb = pp.n[src < 0 ? 0 : src];
+    const int64_t grid = (int64_t)pp.p.B * pp.p.H * ((nb + 15) / 16);
+    hipLaunchKernelGGL((pyramid_kernel<In, NK>), dim3((unsigned)grid), dim3(kSumThreads), lds, stream, pp, src);
+    const int rc = check_launch("pyramid_kernel");
+    if (rc) return rc;
+  }
+  const int64_t g3 = (g2 + kSumThreads / 64 - 1) / (kSumThreads / 64);
+  hipLaunchKernelGGL((range_pyr_kernel<In, NK>), dim3((unsigned)g3), dim3(kSumThreads), 0, stream, pp);
+  return check_launch("range_pyr_kernel");
+}
+
+template <typename In>
+int launch_dyadic_nk(const PyrParams& pp, int64_t g2, hipStream_t stream) {
+  switch (pp.p.D / 64) {
+    case 1: return launch_dyadic<In, 1>(pp, g2, stream);
+    case 2: return launch_dyadic<In, 2>(pp, g2, stream);
+    case 3: return launch_dyadic<In, 3>(pp, g2, stream);
+    default: return launch_dyadic<In, 4>(pp, g2, stream);
+  }
+}
+
 size_t workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t D) {
-  const int64_t nchunks = (T + kChunk - 1) / kChunk;
-  const size_t sums = (size_t)(B * H * nchunks * 2 * D) * sizeof(float);
-  const size_t cnts = (size_t)(B * nchunks) * sizeof(int);
-  const size_t pre = (size_t)(B * H * (nchunks + 1) * 2 * D) * sizeof(double);
-  const size_t cpre = (size_t)(B * (nchunks + 1)) * sizeof(int);
   auto up = [](size_t x) { return ((x + 255) / 256) * 256; };
-  return up(sums) + up(cnts) + up(pre) + cpre;
+  const int64_t nchunks = (T + kChunk - 1) / kChunk;
+  const size_t scalar = up((size_t)(B * H * nchunks * 2 * D) * sizeof(float)) + (size_t)(B * nchunks) * sizeof(int);
+  int64_t E = 0;
+  table_levels(T, nullptr, nullptr, &E);
+  const size_t dyadic = up((size_t)(B * H * E * 2 * D) * sizeof(float)) + (size_t)(B * E) * sizeof(int);
+  return scalar > dyadic ? scalar : dyadic;
 }
 
 }  // namespace
@@ -426,8 +533,6 @@ extern "C" int spruce_kv_summary(const void* k, const int64_t ks[4], const void*
   p.starts = range_starts; p.ends = range_ends;
   auto up = [](size_t x) { return ((x + 255) / 256) * 256; };
   const size_t sums = (size_t)(B * Hkv * p.nchunks * 2 * D) * sizeof(float);
-  const size_t cnts = (size_t)(B * p.nchunks) * sizeof(int);
-  const size_t pre = (size_t)(B * Hkv * (p.nchunks + 1) * 2 * D) * sizeof(double);
   char* ws = static_cast<char*>(workspace);
   p.chunk = reinterpret_cast<float*>(ws);
   p.chunk_cnt = reinterpret_cast<int*>(ws + up(sums));
@@ -435,10 +540,10 @@ extern "C" int spruce_kv_summary(const void* k, const int64_t ks[4], const void*
   const int64_t g1 = B * Hkv * (int64_t)p.nchunks, g2 = B * Hkv * R;
   SPRUCE_REQUIRE(g1 < ((int64_t)1 << 31) && g2 < ((int64_t)1 << 31), "too many workgroups");
   const int eb = dtype == SPRUCE_DTYPE_F32 ? 4 : 2;
-  const bool vec = D % 8 == 0 && 2 * D / 8 <= kMaxGranCols && ks[3] == 1 && vs[3] == 1 &&
-                   ((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0 && (ks[0] * eb) % 16 == 0 &&
-                   (ks[1] * eb) % 16 == 0 && (ks[2] * eb) % 16 == 0 && (vs[0] * eb) % 16 == 0 &&
-                   (vs[1] * eb) % 16 == 0 && (vs[2] * eb) % 16 == 0;
+  const bool vec = D % 64 == 0 && D <= 256 && ks[3] == 1 && vs[3] == 1 && ((uintptr_t)k % 16) == 0 &&
+                   ((uintptr_t)v % 16) == 0 && (ks[0] * eb) % 16 == 0 && (ks[1] * eb) % 16 == 0 &&
+                   (ks[2] * eb) % 16 == 0 && (vs[0] * eb) % 16 == 0 && (vs[1] * eb) % 16 == 0 &&
+                   (vs[2] * eb) % 16 == 0;
   if (!vec) {
     hipLaunchKernelGGL(chunk_sum_kernel, dim3((unsigned)g1), dim3(kSumThreads), 0, (hipStream_t)stream, p);
     int rc = check_launch("chunk_sum_kernel");
@@ -446,20 +551,16 @@ extern "C" int spruce_kv_summary(const void* k, const int64_t ks[4], const void*
     hipLaunchKernelGGL(range_sum_kernel, dim3((unsigned)g2), dim3(kSumThreads), 0, (hipStream_t)stream, p);
     return check_launch("range_sum_kernel");
   }
-  VecParams vp;
-  vp.p = p;
-  vp.prefix = reinterpret_cast<double*>(ws + up(sums) + up(cnts));
-  vp.cnt_prefix = reinterpret_cast<int*>(ws + up(sums) + up(cnts) + up(pre));
-  const size_t lds = (size_t)(17 * 2 * D) * sizeof(float);
-  hipLaunchKernelGGL(chunk_sum_vec_kernel, dim3((unsigned)g1), dim3(kSumThreads), lds, (hipStream_t)stream, vp.p);
-  int rc = check_launch("chunk_sum_vec_kernel");
-  if (rc) return rc;
-  const int64_t ncg = (2 * D + kScanCols - 1) / kScanCols;
-  hipLaunchKernelGGL(chunk_prefix_kernel, dim3((unsigned)(B * Hkv * ncg)), dim3(kSumThreads), 0, (hipStream_t)stream,
-                     vp);
-  rc = check_launch("chunk_prefix_kernel");
-  if (rc) return rc;
-  const int64_t g3 = (g2 + kSumThreads / 64 - 1) / (kSumThreads / 64);
-  hipLaunchKernelGGL(range_sum_vec_kernel, dim3((unsigned)g3), dim3(kSumThreads), 0, (hipStream_t)stream, vp);
-  return check_launch("range_sum_vec_kernel");
+  PyrParams pp;
+  pp.p = p;
+  int64_t n[64], off[64], E = 0;
+  pp.levels = table_levels(T, n, off, &E);
+  SPRUCE_REQUIRE(pp.levels <= kMaxLevels, "sequence too long");
+  for (int i = 0; i < pp.levels; ++i) { pp.n[i] = (int)n[i]; pp.off[i] = (int)off[i]; }
+  pp.E = (int)E;
+  pp.pyr = reinterpret_cast<float*>(ws);
+  pp.pcnt = valid ? reinterpret_cast<int*>(ws + up((size_t)(B * Hkv * E * 2 * D) * sizeof(float))) : nullptr;
+  if (dtype == SPRUCE_DTYPE_BF16) return launch_dyadic_nk<InBF16>(pp, g2, (hipStream_t)stream);
+  if (dtype == SPRUCE_DTYPE_F16) return launch_dyadic_nk<InF16>(pp, g2, (hipStream_t)stream);
+  return launch_dyadic_nk<InF32>(pp, g2, (hipStream_t)stream);
 }

@@ -5,9 +5,10 @@ token_mask=None)`` returns the reference's ``KVSummaryTable``: per tree node
 ``P`` positional prototypes, each the float32 mean of the valid key (value)
 rows of one ``1/P`` slice of the node's token range, with the valid-token
 counts and their logs (-inf for an empty slice).  The sums run in one HIP
-pass over K and V (``spruce_kv_summary``): 64-token chunk sums, then per
-range the covered chunks plus the partial tokens at either end, so upper tree
-levels do not re-read K/V.
+pass over K and V (``spruce_kv_summary``), which builds a dyadic table of
+16-token leaf sums and their pairwise sums; each range then adds the table
+entries that cover it plus its partial leaves, one entry for a tree-node
+prototype range, so upper tree levels do not re-read K/V.
 """
 from __future__ import annotations
 
