@@ -120,6 +120,50 @@ int spruce_sparse_prefill_mask(
     void* out, const int64_t os[4],
     void* stream);
 
+/*
+ * The padded direct-index computation plus residual summaries.  Replaces the
+ * residual_summaries=True branch of sparse_prefill_attention_forward
+ * (sparse/attention.py:163-182, 226-265): each row's softmax also covers one
+ * extra key per (listed tree node, prototype) -- the node's summary key and
+ * value, with log(count) added to its score and no causal mask; prototypes
+ * with count 0 (log count -inf) and nodes < 0 or >= N add nothing.
+ *   nodes        [B, Hkv, Qb, S] int32, strides ns (a layer slice of the
+ *                residual_summary_nodes tensor, trailing -1 padding).
+ *   sum_keys, sum_values  float32 [B, Hkv, N, P, D] contiguous (16-byte
+ *                aligned), sum_log_counts float32 [B, N, P] contiguous: the
+ *                KVSummaryTable spruce_kv_summary writes, N tree nodes.
+ * The summary keys and values are rounded to the MFMA input type (bf16, or
+ * f16 for f16 inputs) like the key blocks.
+ */
+int spruce_sparse_prefill_index_summaries(
+    const void* q, const int64_t qs[4],
+    const void* k, const int64_t ks[4],
+    const void* v, const int64_t vs[4],
+    const int32_t* idx, const int64_t is[4], int64_t K,
+    const int32_t* nodes, const int64_t ns[4], int64_t S,
+    const float* sum_keys, const float* sum_values, const float* sum_log_counts, int64_t N, int64_t P,
+    int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D,
+    float scale, int dtype, int variant,
+    void* out, const int64_t os[4],
+    void* stream);
+
+/*
+ * Residual-tree frontiers.  Replaces build_residual_summary_nodes /
+ * residual_frontier_for_row (interfaces/residual_summaries.py:119-222): for
+ * each row (b, l, g, q) of selected [B, L, G, Qb, K] int32 (element strides
+ * ss[5], any order and duplicates; entries < 0 ignored), the maximal nodes of
+ * the leaf-first binary tree over Qb leaves whose leaf ranges cover the
+ * causal blocks [0, q] the row does not list, ascending by node ID.
+ *   counts int32 [B*L*G*Qb]: frontier size per row, or -1 where the row lists
+ *          an id > q (the reference raises ValueError there).
+ *   out    int32 [B*L*G*Qb, S] contiguous with -1 padding, or NULL with S = 0
+ *          to only count (call once to size S = max(counts), then again).
+ * Qb up to about 250000 (tree bits in 64 KB of LDS).
+ */
+int spruce_residual_frontier(const int32_t* selected, const int64_t ss[5], int64_t B, int64_t L,
+                             int64_t G, int64_t Qb, int64_t K, int32_t* counts, int32_t* out, int64_t S,
+                             void* stream);
+
 /* ------------------------------------------------------------------------
  * Selector front end.  These results are reproducible bit for bit: every
  * float is produced by a fixed sequence of IEEE single-precision operations

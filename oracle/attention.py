@@ -25,6 +25,11 @@ Deliberate, documented choices where the reference has no single answer:
   * ``qblocks_subset`` computes only the listed query blocks (the others stay
     zero), so full-size configurations can be spot-checked row by row.
 
+``sparse_attention_summaries`` restates the residual-summary branch
+(sparse/attention.py:226-265): the row's exact keys plus, for each listed tree
+node and prototype with a non-zero count, the summary key with score
+q . k / sqrt(D) + log(count) and the summary value, in one softmax.
+
 Pinned by tests/test_oracle_attention.py against the reference's own known
 answers (tests/test_sparse_attention.py:32-87 there), an independent dense
 closed form, a pure-Python brute force and structural invariants.
@@ -179,3 +184,58 @@ def attention_bruteforce(q, k, v, key_sets, scale=None):
                 for d in range(D):
                     out[b][t][h][d] = sum(wi * v[b][g][j][d] for wi, j in zip(w, keys)) / z
     return out
+
+
+def sparse_attention_summaries(q, k, v, idx, nodes, sum_keys, sum_values, sum_log_counts,
+                               block_size=64, scale=None, qblocks_subset=None):
+    """Padded lists ``idx [B,Hkv,Qb,K]`` plus summary rows ``nodes [B,Hkv,Qb,S]``
+    over a table ``sum_keys/sum_values [B,Hkv,N,P,D]``, ``sum_log_counts
+    [B,N,P]`` (natural log, -inf for empty prototypes) -> ``[B,T,Hq,D]``."""
+    q = np.asarray(q, dtype=np.float32)
+    k = np.asarray(k, dtype=np.float32)
+    v = np.asarray(v, dtype=np.float32)
+    idx, nodes = np.asarray(idx), np.asarray(nodes)
+    sk = np.asarray(sum_keys, dtype=np.float32)
+    sv = np.asarray(sum_values, dtype=np.float32)
+    sl = np.asarray(sum_log_counts, dtype=np.float32)
+    B, Hq, T, D = q.shape
+    Hkv = k.shape[1]
+    G = Hq // Hkv
+    N = sk.shape[2]
+    def scaled(x):  # the reference divides by sqrt(D) (sparse/attention.py:217-219, 253-256)
+        return x * np.float32(scale) if scale is not None else x / np.float32(math.sqrt(D))
+
+    qblocks = (T + block_size - 1) // block_size
+    out = np.zeros((B, Hq, T, D), dtype=np.float32)
+    offs = np.arange(block_size)
+    for qb in (range(qblocks) if qblocks_subset is None else qblocks_subset):
+        q0, q1 = qb * block_size, min((qb + 1) * block_size, T)
+        q_pos = np.arange(q0, q1)
+        for b in range(B):
+            for g in range(Hkv):
+                ids = np.asarray(idx[b, g, qb], dtype=np.int64)
+                ids = ids[(ids >= 0) & (ids <= qb)]
+                if ids.size == 0:
+                    raise ValueError(
+                        "selected_blocks leaves an attention row empty at "
+                        f"batch={b}, kv_head={g}, query_block={qb}")
+                key_idx = (ids[:, None] * block_size + offs[None, :]).reshape(-1)
+                key_idx = key_idx[key_idx < T]
+                heads = slice(g * G, (g + 1) * G)
+                qh = q[b, heads, q0:q1]
+                s = scaled(np.matmul(qh, k[b, g, key_idx].T))
+                s = np.where((key_idx[None, :] <= q_pos[:, None])[None], s, F32_MIN)
+                vals = v[b, g, key_idx]
+                row = np.asarray(nodes[b, g, qb], dtype=np.int64)
+                row = row[(row >= 0) & (row < N)]
+                if row.size:
+                    keys_s = sk[b, g, row].reshape(-1, D)
+                    vals_s = sv[b, g, row].reshape(-1, D)
+                    bias = sl[b, row].reshape(-1)
+                    keep = np.isfinite(bias)
+                    if keep.any():
+                        ss = scaled(np.matmul(qh, keys_s[keep].T)) + bias[keep][None, None, :]
+                        s = np.concatenate([s, ss.astype(np.float32)], axis=-1)
+                        vals = np.concatenate([vals, vals_s[keep]], axis=0)
+                out[b, heads, q0:q1] = np.matmul(_softmax_rows(s), vals).astype(np.float32)
+    return out.transpose(0, 2, 1, 3).copy()

@@ -12,10 +12,21 @@ Restatements (numpy, float64):
                   count, log(count) or -inf.  Direct float64 sums.
   prefix_summary  the same table by the reference's own method (differences
                   of prefix sums, :105-122), used to cross-check kv_summary.
+  frontier_visit  residual_frontier_for_row (interfaces/residual_summaries.py:
+                  119-147): the top-down visit from the root that keeps a node
+                  when its range is causal and holds no listed block, else
+                  recurses into its children; sorted by node ID.
+  frontier_dyadic an independent construction of the same set: every gap
+                  between listed blocks, cut greedily from its left end into
+                  the largest tree node that starts there and fits.
 
 Pinned by tests/test_oracle_summaries.py: the reference's known answers
 (tests/test_residual_summaries.py:25-41 and tests/test_summary_pooling.py:49-88
-in the reference) and the agreement of the two summation methods.
+in the reference) and the agreement of the two summation methods.  The two
+frontier constructions are pinned by the reference's frontier known answers
+(tests/test_residual_summaries.py:44-64 there), by agreeing with each other,
+and by the partition and maximality properties checked from first principles
+(tests/test_oracle_frontier.py).
 """
 import numpy as np
 
@@ -96,3 +107,63 @@ def prefix_summary(key, value, rs, re, valid=None):
     with np.errstate(divide="ignore"):
         logc = np.where(counts > 0, np.log(np.maximum(counts, 1e-300)), -np.inf)
     return pool(key) / den, pool(value) / den, counts, logc
+
+
+def frontier_visit(selected, qb, layout):
+    """Maximal tree nodes covering the causal blocks [0, qb] not in `selected`.
+
+    layout: the dict of tree_layout().  Raises ValueError for a listed id > qb,
+    as the reference does."""
+    listed = sorted({int(b) for b in selected if int(b) >= 0})
+    if listed and listed[-1] > qb:
+        raise ValueError("selected block IDs must be causal and non-negative")
+    starts, ends, levels, indices = (layout[f] for f in ("starts", "ends", "levels", "indices"))
+    counts, offsets = layout["level_counts"], layout["level_offsets"]
+    listed_set = set(listed)
+    out = []
+
+    def visit(node):
+        s, e = starts[node], ends[node]
+        if s > qb:
+            return
+        if e <= qb + 1 and not any(j in listed_set for j in range(s, e)):
+            out.append(node)
+            return
+        lvl = levels[node]
+        if lvl == 0:
+            return
+        for c in (2 * indices[node], 2 * indices[node] + 1):
+            if c < counts[lvl - 1]:
+                visit(offsets[lvl - 1] + c)
+
+    visit(offsets[-1])
+    return sorted(out)
+
+
+def frontier_dyadic(selected, qb, num_leaves):
+    """Same set by greedy decomposition of each gap [a, b) between listed blocks.
+
+    From a, take the highest-level node that starts at a (a divisible by its
+    width) and ends (clipped to num_leaves) at or before b; repeat from its
+    end.  Node (level v, index i) has ID sum of the level counts below v, + i."""
+    listed = sorted({int(b) for b in selected if 0 <= int(b) <= qb})
+    counts = [num_leaves]
+    while counts[-1] > 1:
+        counts.append((counts[-1] + 1) // 2)
+    offsets = [sum(counts[:v]) for v in range(len(counts))]
+    gaps, prev = [], -1
+    for j in listed + [qb + 1]:
+        if j > prev + 1:
+            gaps.append((prev + 1, j))
+        prev = j
+    out = []
+    for a, b in gaps:
+        pos = a
+        while pos < b:
+            v = 0
+            while (v + 1 < len(counts) and pos % (1 << (v + 1)) == 0
+                   and min(pos + (1 << (v + 1)), num_leaves) <= b):
+                v += 1
+            out.append(offsets[v] + (pos >> v))
+            pos = min(pos + (1 << v), num_leaves)
+    return sorted(out)

@@ -62,6 +62,16 @@ struct AttnParams {
   const uint8_t* mask;
   int64_t ms[4];
   int mask_per_qhead;
+  // residual summaries (sparse/attention.py:226-265): per row, nodes
+  // [B, Hkv, Qb, S] int32 (-1 = none); table keys/values float32
+  // [B, Hkv, N, P, D] and natural-log counts [B, N, P], all contiguous.
+  const int32_t* snode;
+  int64_t sns[4];
+  int S, N, P;
+  const float* skey;
+  const float* sval;
+  const float* slog;
+  float sbias;  // log counts -> raw score units: log2(e) / cs
 };
 
 struct F32x8 {
@@ -263,13 +273,27 @@ __device__ __forceinline__ uint32_t word_of(const uint4& r, int k) {
   return k == 0 ? r.x : k == 1 ? r.y : k == 2 ? r.z : r.w;
 }
 
+// Writes dims [8 bd, 8 bd + 8) of four consecutive keys (r0..r3, eight 16-bit
+// MFMA inputs each) into the V^T tile: dim e of the four keys becomes one
+// 8-byte row segment at dst + e * vstride (two v_perm_b32 per segment).
+__device__ __forceinline__ void store_vt4(uint16_t* dst, int vstride, const uint4& r0, const uint4& r1,
+                                          const uint4& r2, const uint4& r3) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+    const uint32_t w0 = __builtin_amdgcn_perm(word_of(r1, e >> 1), word_of(r0, e >> 1), sel);
+    const uint32_t w1 = __builtin_amdgcn_perm(word_of(r3, e >> 1), word_of(r2, e >> 1), sel);
+    *reinterpret_cast<uint2*>(dst + e * vstride) = uint2{w0, w1};
+  }
+}
+
 // Softmax reference point: the running max is only raised when a row's max
 // grows by more than this (log2 units), so most blocks skip the O rescale.
 // Exponents stay <= 2^8, far inside fp32/bf16/f16 range; the final O / l is
 // unchanged because O and l share the same reference point.
 constexpr float kRescaleThreshold = 8.0f;
 
-template <int D, int WAVES, typename TIn, bool F16, int MODE>
+template <int D, int WAVES, typename TIn, bool F16, int MODE, bool SUMM = false>
 __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnParams p) {
   constexpr int NTHR = WAVES * 64;
   constexpr int KSTR = D + 8;        // K tile row stride, 16-bit elements (16 B pad)
@@ -394,14 +418,7 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
         const uint4 r1 = raw_to_mfma<TIn, F16>(vst[i][1]);
         const uint4 r2 = raw_to_mfma<TIn, F16>(vst[i][2]);
         const uint4 r3 = raw_to_mfma<TIn, F16>(vst[i][3]);
-        // Dim e of the four keys -> one 8-byte V^T row segment (v_perm_b32 x2).
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-          const uint32_t w0 = __builtin_amdgcn_perm(word_of(r1, e >> 1), word_of(r0, e >> 1), sel);
-          const uint32_t w1 = __builtin_amdgcn_perm(word_of(r3, e >> 1), word_of(r2, e >> 1), sel);
-          *reinterpret_cast<uint2*>(Vt + vlds[i] + e * VSTR) = uint2{w0, w1};
-        }
+        store_vt4(Vt + vlds[i], VSTR, r0, r1, r2, r3);
       }
     }
   };
@@ -412,7 +429,8 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16_t{};
 
-  auto compute = [&](int buf, bool diag) {
+  // sb: per-key score bias of a summary chunk (null for a key block).
+  auto compute = [&](int buf, bool diag, const float* sb) {
     const uint16_t* Ks = smem + buf * BUF;
     const uint16_t* Vt = Ks + KTILE;
     // S^T (64 keys x 32 queries) as two 32x32 tiles, LDS reads one k-step ahead.
@@ -443,6 +461,18 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
         if (32 + kr > thr) s1[r] = -INFINITY;
       }
     }
+    if (sb != nullptr) {
+      // Summary keys: add log(count) in raw score units; no causal mask
+      // (sparse/attention.py:252-258).  Register 4j+t of key tile c holds
+      // key 32c + 8j + 4(lane/32) + t.
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 b0 = *reinterpret_cast<const float4*>(sb + 8 * j + 4 * hl);
+        const float4 b1 = *reinterpret_cast<const float4*>(sb + 32 + 8 * j + 4 * hl);
+        s0[4 * j] += b0.x; s0[4 * j + 1] += b0.y; s0[4 * j + 2] += b0.z; s0[4 * j + 3] += b0.w;
+        s1[4 * j] += b1.x; s1[4 * j + 1] += b1.y; s1[4 * j + 2] += b1.z; s1[4 * j + 3] += b1.w;
+      }
+    }
     float mx = fmaxf(s0[0], s0[1]);
 #pragma unroll
     for (int r = 2; r < 16; ++r) mx = fmaxf(mx, s0[r]);
@@ -460,7 +490,9 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[dt][r] *= alpha;
     }
-    const float nm = -m_use;
+    // A lane whose keys so far are all -inf (a summary-only row) keeps
+    // m_use = -inf; exp2(-inf) = 0 needs a finite offset there.
+    const float nm = (sb != nullptr && m_use == -INFINITY) ? 0.f : -m_use;
     float psum = 0.f;
     uint4 pk[2][2];
 #pragma unroll
@@ -502,23 +534,80 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
   it.init(p, b, g, qb, part, hq, lane);
   int cur_id = 0;
   bool cur_en = false;
+  int buf = 0;
   if (it.next(cur_id, cur_en)) {
     load_block(cur_id);
     store_block(0);
     __syncthreads();
-    int buf = 0;
     while (true) {
       int nid = 0;
       bool nen = false;
       const bool more = it.next(nid, nen);
       if (more) load_block(nid);
-      if (active && cur_en) compute(buf, cur_id == qb);
+      if (active && cur_en) compute(buf, cur_id == qb, nullptr);
       if (!more) break;
       store_block(buf ^ 1);
       __syncthreads();
       buf ^= 1;
       cur_id = nid;
       cur_en = nen;
+    }
+  }
+
+  if constexpr (SUMM) {
+    // Residual summaries of the row: entry e is prototype e % P of the
+    // row's (e / P)-th node, appended after the exact keys as chunks of 64
+    // keys (sparse/attention.py:232-265).  Missing nodes and empty prototypes
+    // get a -inf bias, so they add exactly zero weight.
+    __shared__ __attribute__((aligned(16))) float sbias[2][kBlock];
+    const int32_t* nrow = p.snode + (int64_t)b * p.sns[0] + (int64_t)g * p.sns[1] + (int64_t)qb * p.sns[2];
+    int nn = 0;  // one past the last listed node (uniform)
+    for (int j0 = 0; j0 < p.S; j0 += 64) {
+      const int j = j0 + lane;
+      const int v = j < p.S ? nrow[(int64_t)j * p.sns[3]] : -1;
+      const uint64_t m = __ballot(v >= 0 && v < p.N);
+      if (m) nn = j0 + 64 - __builtin_clzll(m);
+    }
+    const int E = nn * p.P;
+    const int64_t bg = (int64_t)b * p.Hkv + g;
+    auto node_of = [&](int en) {
+      if (en >= E) return -1;
+      const int v = nrow[(int64_t)(en / p.P) * p.sns[3]];
+      return (v >= 0 && v < p.N) ? v : -1;
+    };
+    auto load_row8 = [&](const float* base, int en, int node, int d0) {
+      if (node < 0) return uint4{0u, 0u, 0u, 0u};
+      const float4* s = reinterpret_cast<const float4*>(
+          base + ((bg * p.N + node) * p.P + en % p.P) * (int64_t)D + d0);
+      const float4 x = s[0], y = s[1];
+      return uint4{pack2<F16>(x.x, x.y), pack2<F16>(x.z, x.w), pack2<F16>(y.x, y.y), pack2<F16>(y.z, y.w)};
+    };
+    for (int e0 = 0; e0 < E; e0 += kBlock) {
+      buf ^= 1;  // its last reader finished before the previous barrier
+      uint16_t* Ks = smem + buf * BUF;
+      uint16_t* Vt = Ks + KTILE;
+      for (int c = tid; c < KCHUNKS; c += NTHR) {
+        const int key = c / KROWCH, dc = c % KROWCH;
+        const int en = e0 + key;
+        *reinterpret_cast<uint4*>(Ks + key * KSTR + dc * 8) = load_row8(p.skey, en, node_of(en), dc * 8);
+      }
+      for (int t = tid; t < VTASKS; t += NTHR) {
+        const int a = t & 15, bd = t >> 4;
+        uint4 r[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int en = e0 + 4 * a + j;
+          r[j] = load_row8(p.sval, en, node_of(en), bd * 8);
+        }
+        store_vt4(Vt + 8 * bd * VSTR + vt_pos(4 * a), VSTR, r[0], r[1], r[2], r[3]);
+      }
+      if (tid < kBlock) {
+        const int en = e0 + tid;
+        const int node = node_of(en);
+        sbias[buf][tid] = node < 0 ? -INFINITY : p.slog[((int64_t)b * p.N + node) * p.P + en % p.P] * p.sbias;
+      }
+      __syncthreads();
+      if (active) compute(buf, false, sbias[buf]);
     }
   }
 
@@ -569,37 +658,37 @@ inline LaunchShape choose_shape(int variant, int G) {
   return {4, (tiles + 3) / 4};
 }
 
-template <int D, int WAVES, typename TIn, bool F16, int MODE>
+template <int D, int WAVES, typename TIn, bool F16, int MODE, bool SUMM>
 int launch_attention_t(const AttnParams& p, hipStream_t stream) {
   // Rows are padded to a multiple of the 8 XCDs; the extra workgroups exit.
   const int64_t rows8 = ((int64_t)p.B * p.Hkv * p.Qb + 7) / 8 * 8;
   const int64_t grid = rows8 * p.parts;
-  hipLaunchKernelGGL((sparse_prefill_kernel<D, WAVES, TIn, F16, MODE>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((sparse_prefill_kernel<D, WAVES, TIn, F16, MODE, SUMM>), dim3((unsigned)grid),
                      dim3(WAVES * 64), 0, stream, p);
   return check_launch("sparse_prefill_kernel");
 }
 
-template <int MODE, int D, typename TIn, bool F16>
+template <int MODE, bool SUMM, int D, typename TIn, bool F16>
 int launch_attention_w(const AttnParams& p, int waves, hipStream_t stream) {
   switch (waves) {
-    case 2: return launch_attention_t<D, 2, TIn, F16, MODE>(p, stream);
-    case 4: return launch_attention_t<D, 4, TIn, F16, MODE>(p, stream);
-    case 7: return launch_attention_t<D, 7, TIn, F16, MODE>(p, stream);
-    case 8: return launch_attention_t<D, 8, TIn, F16, MODE>(p, stream);
+    case 2: return launch_attention_t<D, 2, TIn, F16, MODE, SUMM>(p, stream);
+    case 4: return launch_attention_t<D, 4, TIn, F16, MODE, SUMM>(p, stream);
+    case 7: return launch_attention_t<D, 7, TIn, F16, MODE, SUMM>(p, stream);
+    case 8: return launch_attention_t<D, 8, TIn, F16, MODE, SUMM>(p, stream);
     default: return set_error(SPRUCE_EINVAL, "unsupported wave count %d", waves);
   }
 }
 
-template <int MODE>
+template <int MODE, bool SUMM = false>
 int launch_attention(const AttnParams& p, int D, int dtype, int waves, hipStream_t stream) {
   if (D == 128) {
-    if (dtype == SPRUCE_DTYPE_BF16) return launch_attention_w<MODE, 128, InBF16, false>(p, waves, stream);
-    if (dtype == SPRUCE_DTYPE_F16) return launch_attention_w<MODE, 128, InF16, true>(p, waves, stream);
-    return launch_attention_w<MODE, 128, InF32, false>(p, waves, stream);
+    if (dtype == SPRUCE_DTYPE_BF16) return launch_attention_w<MODE, SUMM, 128, InBF16, false>(p, waves, stream);
+    if (dtype == SPRUCE_DTYPE_F16) return launch_attention_w<MODE, SUMM, 128, InF16, true>(p, waves, stream);
+    return launch_attention_w<MODE, SUMM, 128, InF32, false>(p, waves, stream);
   }
-  if (dtype == SPRUCE_DTYPE_BF16) return launch_attention_w<MODE, 64, InBF16, false>(p, waves, stream);
-  if (dtype == SPRUCE_DTYPE_F16) return launch_attention_w<MODE, 64, InF16, true>(p, waves, stream);
-  return launch_attention_w<MODE, 64, InF32, false>(p, waves, stream);
+  if (dtype == SPRUCE_DTYPE_BF16) return launch_attention_w<MODE, SUMM, 64, InBF16, false>(p, waves, stream);
+  if (dtype == SPRUCE_DTYPE_F16) return launch_attention_w<MODE, SUMM, 64, InF16, true>(p, waves, stream);
+  return launch_attention_w<MODE, SUMM, 64, InF32, false>(p, waves, stream);
 }
 
 // Shared argument checks and parameter setup of the three entry points.

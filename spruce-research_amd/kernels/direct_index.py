@@ -85,6 +85,52 @@ def direct_index_sparse_prefill(q, k, v, indices, scale, block_size=64,
     return out
 
 
+def direct_index_sparse_summaries(q, k, v, indices, nodes, table, scale, block_size=64,
+                                  kernel_variant="single_head"):
+    """Direct-index attention plus residual summaries (sparse/attention.py:226-265).
+
+    indices: int32 ``[B,Hkv,ceil(T/64),K]``; nodes: int32 ``[B,Hkv,ceil(T/64),S]``
+    residual tree-node IDs (-1 padding); table: the ``KVSummaryTable`` of
+    ``sparse.summaries.build_kv_summary_table`` over the same K/V (keys/values
+    ``[B,Hkv,N,P,D]`` float32, log_counts ``[B,N,P]``).  Every listed node adds
+    one softmax entry per prototype with a non-empty slice: the summary key's
+    score plus log(count), and the summary value.  Returns ``[B,T,Hq,D]``.
+    """
+    B, Hq, Hkv, T, D = _check_common(q, k, v, block_size, kernel_variant)
+    qblocks = (T + block_size - 1) // block_size
+    if indices.dim() != 4 or tuple(indices.shape[:3]) != (B, Hkv, qblocks) or indices.dtype != torch.int32:
+        raise ValueError("indices must be int32 [B,Hkv,ceil(T/64),K]")
+    if nodes.dim() != 4 or tuple(nodes.shape[:3]) != (B, Hkv, qblocks) or nodes.dtype != torch.int32:
+        raise ValueError("residual nodes must be int32 [B,Hkv,ceil(T/64),S]")
+    keys, values, logc = table.keys, table.values, table.log_counts
+    if keys.dim() != 5 or keys.shape[:2] != (B, Hkv) or keys.shape[4] != D or values.shape != keys.shape:
+        raise ValueError("summary keys/values must be float32 [B,Hkv,N,P,D]")
+    if logc.shape != (B, keys.shape[2], keys.shape[3]):
+        raise ValueError("summary log_counts must be [B,N,P]")
+    if any(t.dtype != torch.float32 or not t.is_contiguous() for t in (keys, values, logc)):
+        raise ValueError("summary tables must be contiguous float32")
+    if any(x.stride(-1) != 1 for x in (q, k, v, indices, nodes)):
+        raise ValueError("q, k, v, indices and nodes must have a contiguous final dimension")
+    if any(t.device != q.device for t in (indices, nodes, keys, values, logc)):
+        raise ValueError("indices, nodes and the summary table must be on the same device as q")
+    out, out_strides = _output(q)
+    with torch.cuda.device(q.device):
+        rc = spruce_hip.lib().spruce_sparse_prefill_index_summaries(
+            spruce_hip.ptr(q), spruce_hip.strides(q),
+            spruce_hip.ptr(k), spruce_hip.strides(k),
+            spruce_hip.ptr(v), spruce_hip.strides(v),
+            spruce_hip.ptr(indices), spruce_hip.strides(indices), indices.shape[3],
+            spruce_hip.ptr(nodes), spruce_hip.strides(nodes), nodes.shape[3],
+            spruce_hip.ptr(keys), spruce_hip.ptr(values), spruce_hip.ptr(logc),
+            keys.shape[2], keys.shape[3],
+            B, Hq, Hkv, T, D, float(scale), spruce_hip.dtype_code(q),
+            spruce_hip.variant_code(kernel_variant),
+            spruce_hip.ptr(out), out_strides, spruce_hip.stream_of(q))
+    spruce_hip.check(rc, "spruce_sparse_prefill_index_summaries")
+    _record(kernel_variant, Hq, Hkv, D)
+    return out
+
+
 def direct_index_sparse_csr(q, k, v, indptr, indices, scale, block_size=64,
                             row_order=None, kernel_variant="single_head"):
     """Causal block-sparse attention over variable-length (CSR) block lists.

@@ -8,19 +8,27 @@ host loop of small PyTorch ops; here the whole layer is one launch of the
 gfx950 direct-index kernel, which reads ``selected_blocks[:, layer_idx]`` in
 place.
 
+With ``residual_summaries=True`` the row's softmax also covers the summary
+keys of its residual tree nodes (sparse/attention.py:163-182, 226-265): the
+summary table of the layer's K/V is built on the GPU
+(``build_kv_summary_table``) and the same kernel appends one key per listed
+node and non-empty prototype, scored q.k/sqrt(D) + log(count).
+
 Differences, all raising instead of computing something else:
   * ``block_size`` must be 64 and ``head_dim`` 64 or 128 (the kernel's tile);
   * ``attention_mask`` must be None (B=1 unpadded prefill; causality is
-    applied by the kernel), as in the reference's kernel backend;
-  * ``residual_summaries=True`` raises NotImplementedError.
+    applied by the kernel), as in the reference's kernel backend.
 """
 import math
 from typing import Optional
 
 import torch
 
+from interfaces.residual_summaries import (build_residual_tree_layout,
+                                          validate_residual_summary_nodes)
 from interfaces.validator import validate_selected_blocks
-from kernels.direct_index import direct_index_sparse_prefill
+from kernels.direct_index import direct_index_sparse_prefill, direct_index_sparse_summaries
+from sparse.summaries import build_kv_summary_table
 
 SPARSE_PREFILL_ATTENTION = "spruce_sparse_prefill"
 SUMMARY_PROTOTYPES = (1, 2, 4)
@@ -106,8 +114,20 @@ def sparse_prefill_attention_forward(
     if summary_mode not in SUMMARY_MODES:
         raise ValueError(f"summary_mode must be one of {SUMMARY_MODES}, got {summary_mode!r}")
     if residual_summaries:
-        raise NotImplementedError(
-            "residual summaries are not implemented in the HIP sparse-prefill path")
+        if residual_summary_nodes is None:
+            raise ValueError(
+                "residual_summaries=True requires residual_summary_nodes; "
+                "construct the complete frontier before model forward")
+        if summary_mode == "learned":
+            if not summary_checkpoint:
+                raise ValueError("summary_mode='learned' requires summary_checkpoint")
+            raise NotImplementedError(
+                "The learned compressor is gated on deterministic-summary "
+                "evaluation and is not implemented before that gate passes.")
+        if validate_residual_summary_nodes_input:
+            validate_residual_summary_nodes(
+                selected_blocks, residual_summary_nodes,
+                validate_selected=not validate_selected_blocks_input)
     if attention_mask is not None:
         if attention_mask.dim() != 4:
             raise ValueError(
@@ -127,8 +147,21 @@ def sparse_prefill_attention_forward(
             "selected_blocks leaves an attention row empty at "
             f"batch={b}, layer={layer_idx}, kv_head={g}, query_block={qb}")
     D = query.shape[-1]
-    output = direct_index_sparse_prefill(
-        query, key, value, indices, scale=1.0 / math.sqrt(D), block_size=block_size)
+    if not residual_summaries:
+        output = direct_index_sparse_prefill(
+            query, key, value, indices, scale=1.0 / math.sqrt(D), block_size=block_size)
+        return output, None
+    # Residual summaries (sparse/attention.py:163-182): the frontier nodes of
+    # this layer, and the summary table of this layer's K/V over the tree.
+    if residual_summary_nodes.shape[:4] != selected_blocks.shape[:4]:
+        raise ValueError(
+            "residual_summary_nodes must match selected_blocks through the query-block dimension")
+    nodes = residual_summary_nodes[:, layer_idx].to(device=query.device, dtype=torch.int32).contiguous()
+    layout = build_residual_tree_layout(indices.shape[2])
+    table = build_kv_summary_table(key, value, layout, block_size=block_size,
+                                   prototypes=summary_prototypes)
+    output = direct_index_sparse_summaries(
+        query, key, value, indices, nodes, table, scale=1.0 / math.sqrt(D), block_size=block_size)
     return output, None
 
 

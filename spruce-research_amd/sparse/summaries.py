@@ -125,3 +125,41 @@ def token_validity_from_attention_mask(attention_mask: torch.Tensor | None, *, b
     if attention_mask.shape[0] != batch or attention_mask.shape[-1] != seq_len:
         raise ValueError("attention mask batch/key dimensions do not match K/V")
     return (attention_mask[:, 0] >= 0).any(dim=-2)
+
+
+def residual_attention_density(selected_blocks: torch.Tensor, residual_summary_nodes: torch.Tensor, *,
+                               seq_len: int, block_size: int, prototypes: int) -> dict:
+    """Attention entries a route charges (sparse/summaries.py:166-226):
+    block_size per listed exact block plus one entry per listed node prototype
+    whose token slice is non-empty, against the dense causal maximum."""
+    if selected_blocks.dim() != 5 or residual_summary_nodes.dim() != 5:
+        raise ValueError("selected and residual routes must both be 5D")
+    if selected_blocks.shape[:4] != residual_summary_nodes.shape[:4]:
+        raise ValueError("selected and residual routes must match through Q")
+    if prototypes not in SUMMARY_PROTOTYPES:
+        raise ValueError(f"prototypes must be one of {SUMMARY_PROTOTYPES}, got {prototypes}")
+    batch, layers, groups, query_blocks, _ = selected_blocks.shape
+    if query_blocks != (seq_len + block_size - 1) // block_size:
+        raise ValueError("sequence length and route query-block count disagree")
+    from interfaces.residual_summaries import build_residual_tree_layout
+
+    tree = build_residual_tree_layout(query_blocks)
+    first = (torch.tensor(tree.starts, dtype=torch.long) * block_size).clamp_max(seq_len)
+    last = (torch.tensor(tree.ends, dtype=torch.long) * block_size).clamp_max(seq_len)
+    # A node of n tokens split into P slices has min(P, n) non-empty ones.
+    per_node = (last - first).clamp_max(prototypes)
+    exact = int((selected_blocks >= 0).sum().item()) * block_size
+    ids = residual_summary_nodes.detach().to(device="cpu", dtype=torch.long)
+    ids = ids[ids >= 0]
+    summary = int(per_node[ids].sum().item()) if ids.numel() else 0
+    charged = exact + summary
+    maximum = batch * layers * groups * query_blocks * (query_blocks + 1) // 2 * block_size
+    fraction = charged / maximum if maximum else 0.0
+    return {
+        "exact_attention_entries": exact,
+        "summary_prototype_entries": summary,
+        "charged_attention_entries": charged,
+        "maximum_causal_attention_entries": maximum,
+        "charged_attention_fraction": fraction,
+        "charged_sparsity": 1.0 - fraction,
+    }

@@ -61,6 +61,12 @@ _SIGNATURES = {
         _p, _STRIDES, _p, _STRIDES, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _p, _p, _i64,
         _p, _p, _p, _p, _p, ctypes.c_size_t, _p],
     "spruce_group_avg_tokens": [_p, _STRIDES, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _p],
+    "spruce_sparse_prefill_index_summaries": [
+        _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _i64,
+        _p, _STRIDES, _i64, _p, _p, _p, _i64, _i64,
+        _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int, ctypes.c_int,
+        _p, _STRIDES, _p],
+    "spruce_residual_frontier": [_p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p],
     "spruce_sparse_prefill_mask": [
         _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _i64,
         _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int, ctypes.c_int,
@@ -119,6 +125,13 @@ def strides(t, order=None):
     if len(s) != 4:
         raise ValueError(f"expected a 4-D tensor, got {t.dim()}-D")
     return (_i64 * 4)(*s)
+
+
+def strides5(t):
+    """int64[5] element strides of a 5-D tensor."""
+    if t.dim() != 5:
+        raise ValueError(f"expected a 5-D tensor, got {t.dim()}-D")
+    return (_i64 * 5)(*t.stride())
 
 
 def ptr(t):
