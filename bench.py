@@ -257,7 +257,7 @@ def main():
             "tflops": round(fl4 / (m4 * 1e-3) / 1e12, 2),
             "frac_bf16_peak": round(fl4 / (m4 * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
             "flop": fl4, "top_k": 8,
-            "note": "algorithmic FLOP = QK^T once over causal blocks; the kernel runs QK^T twice",
+            "note": "algorithmic FLOP = QK^T once over causal blocks (the single-pass kernel computes it once)",
         }
         del q4, k4
 

@@ -222,10 +222,16 @@ int spruce_causal_topk(const float* scores, int64_t R, int64_t Qb, int64_t Kb, i
  * Teacher target extraction.
  * ---------------------------------------------------------------------- */
 
-/* Bytes of device workspace spruce_teacher_block_mass needs:
- * row statistics [B, Hq, T, 2] plus per-half tile partials [B, Hq, 2, Qb, Qb]
- * float32, Qb = ceil(T/64). */
+/* Device workspace of spruce_teacher_block_mass, Qb = ceil(T/64).
+ * _min: the two-pass schedule -- row statistics [B, Hq, T, 2] plus per-half
+ *   tile partials [B, Hq, 2, Qb, Qb] float32; QK^T is computed twice.
+ * spruce_teacher_workspace_bytes: the preferred size.  While
+ *   B*Hq*Qb*(Qb+1)*256 <= 4 GiB it adds the single-pass scratch (each row's
+ *   per-key-block partial sum and reference max, 8 bytes per row and block)
+ *   and a workspace of at least this size selects the single pass, which
+ *   computes QK^T once; otherwise it equals _min. */
 size_t spruce_teacher_workspace_bytes(int64_t B, int64_t Hq, int64_t T);
+size_t spruce_teacher_workspace_bytes_min(int64_t B, int64_t Hq, int64_t T);
 
 /*
  * Dense causal softmax attention reduced to block probability mass without

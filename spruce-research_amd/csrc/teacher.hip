@@ -15,13 +15,22 @@
 // rounds QK^T to the model dtype before its float32 softmax,
 // teacher/chunked_extract.py:119,126).
 //
-// Two passes over the causal (I, J) tiles, GQA-packed like the sparse prefill
+// The causal (I, J) tiles are walked GQA-packed like the sparse prefill
 // kernel (one workgroup per (batch, KV head, query block, part), one 32-row
-// tile of one query head per wave, K blocks staged once per workgroup in LDS):
-//   pass 1: running row max and softmax denominator per query row;
-//   pass 2: recomputed scores -> exp(s - m) / l summed over each 64x64 tile,
-//           one float per (tile half, J) into a [B, H, 2, Qb, Qb] workspace;
-//   combine: mass = half0 + half1 (exactly two addends, order-independent).
+// tile of one query head per wave, K blocks staged once per workgroup in LDS).
+// A row's mass needs its final softmax denominator l before its 64 rows are
+// summed, so one of two schedules is used:
+//   single pass (when its scratch fits, see kSinglePassScratchMax): online
+//     row max / denominator as in attention, and for every J the row's
+//     partial sum e_J = sum_j exp2(s_j - m_J) with its reference point m_J
+//     written to scratch (8 bytes per row and J); once the row is complete
+//     the wave reads them back and sums e_J * exp2(m_J - m) / l over its 32
+//     rows in a fixed butterfly order.  QK^T runs once.
+//   two passes (longer sequences): pass 1 keeps only the row max and
+//     denominator; pass 2 recomputes the scores and sums exp(s - m) / l over
+//     each 32-row x 64-key tile.  QK^T runs twice.
+// Both write one float per (tile half, J) into a [B, H, 2, Qb, Qb] workspace;
+// mass = half0 + half1 (exactly two addends, order-independent).
 #include "attention_impl.h"
 
 namespace spruce {
@@ -32,9 +41,18 @@ struct MassParams {
   int64_t qs[4], ks[4];
   int B, Hq, Hkv, T, G, Qb, parts;
   float cs;     // scale * log2(e)
-  float* stats;  // [B, Hq, T, 2]: (row max in log2 units, row sum)
+  float* stats;  // [B, Hq, T, 2]: (row max in log2 units, row sum), two-pass only
   float* part;   // [B, Hq, 2, Qb, Qb]
+  float2* rowj;  // single pass: [B, Hq, 2, Qb(Qb+1)/2, 32] (e_J, m_J) per row
 };
+
+// Single-pass scratch is B*Hq*Qb*(Qb+1)*256 bytes (471 MB at T=16K, 28 heads);
+// above this the two-pass schedule is used instead.
+constexpr int64_t kSinglePassScratchMax = (int64_t)4 << 30;
+
+inline int64_t single_pass_scratch_bytes(int64_t B, int64_t Hq, int64_t Qb) {
+  return B * Hq * Qb * (Qb + 1) * 256;
+}
 
 template <int D, int WAVES, typename TIn, bool F16, int PASS>
 __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams p) {
@@ -117,6 +135,11 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
     inv_l = 1.f / stat[1];
   }
   float* part_out = p.part + ((((int64_t)b * p.Hq + head) * 2 + half) * p.Qb + qb) * p.Qb;
+  // Single pass: this tile's (e_J, m_J) rows, J = 0..qb, 32 rows each.
+  float2* rowj = nullptr;
+  if (PASS == 3)
+    rowj = p.rowj + ((((int64_t)b * p.Hq + head) * 2 + half) * ((int64_t)p.Qb * (p.Qb + 1) / 2) +
+                     (int64_t)qb * (qb + 1) / 2) * 32;
 
   load_k(0);
   store_k(0);
@@ -151,7 +174,7 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
           if (32 + kr > thr) s1[r] = -INFINITY;
         }
       }
-      if (PASS == 1) {
+      if (PASS == 1 || PASS == 3) {
         float mx = fmaxf(s0[0], s0[1]);
 #pragma unroll
         for (int r = 2; r < 16; ++r) mx = fmaxf(mx, s0[r]);
@@ -169,6 +192,10 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
 #pragma unroll
         for (int r = 0; r < 16; ++r) ps += fast_exp2(fmaf(s0[r], p.cs, nm)) + fast_exp2(fmaf(s1[r], p.cs, nm));
         l_run += ps;
+        if (PASS == 3) {
+          const float e = ps + __shfl_xor(ps, 32);
+          if (hl == 0) rowj[(int64_t)J * 32 + l32] = float2{e, m_use};
+        }
       } else {
         const float nm = -m_use;
         float ps = 0.f;
@@ -191,6 +218,38 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
     if (hl == 0 && qtok < p.T) {
       stat[0] = m_use;
       stat[1] = lt;
+    }
+  }
+  if (PASS == 3 && active) {
+    const float lt = l_run + __shfl_xor(l_run, 32);
+    const float inv = (qtok < p.T && lt > 0.f) ? 1.f / lt : 0.f;
+    // The wave reads back only what it wrote, on the same CU: a
+    // workgroup-scope fence (wait for the stores) orders them before the
+    // loads.  An agent-scope fence would also write back this XCD's L2.
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    // 16 key blocks per step, all loads issued first: lane half hl takes
+    // J = J0 + 2u + hl (u = 0..7), lane l32 row l32; each J is then summed
+    // over the 32 rows by a fixed butterfly.
+    constexpr int U = 8;
+    for (int J0 = 0; J0 <= qb; J0 += 2 * U) {
+      float2 em[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int J = J0 + 2 * u + hl;
+        em[u] = J <= qb ? rowj[(int64_t)J * 32 + l32] : float2{0.f, m_use};
+      }
+      float v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = em[u].x * fast_exp2(em[u].y - m_use) * inv;
+#pragma unroll
+      for (int off = 16; off >= 1; off >>= 1)
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] += __shfl_xor(v[u], off);
+      if (l32 == 0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (J0 + 2 * u + hl <= qb) part_out[J0 + 2 * u + hl] = v[u];
+      }
     }
   }
 }
@@ -365,7 +424,7 @@ extern "C" int spruce_teacher_block_mass(const void* q, const int64_t qs[4], con
   if (rc) return rc;
   SPRUCE_REQUIRE(mass != nullptr && workspace != nullptr, "mass and workspace must be non-null");
   const int64_t Qb = (T + kBlock - 1) / kBlock;
-  const size_t need = spruce_teacher_workspace_bytes(B, Hq, T);
+  const size_t need = spruce_teacher_workspace_bytes_min(B, Hq, T);
   SPRUCE_REQUIRE(workspace_bytes >= need, "workspace too small: %zu bytes, need %zu", workspace_bytes, need);
   SPRUCE_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, "workspace must be 16-byte aligned");
   MassParams p{};
@@ -383,22 +442,40 @@ extern "C" int spruce_teacher_block_mass(const void* q, const int64_t qs[4], con
   p.Qb = (int)Qb;
   p.parts = shape.parts;
   p.cs = scale * 1.4426950408889634f;
-  p.stats = workspace;
-  p.part = workspace + (size_t)B * Hq * T * 2;
   hipStream_t s = (hipStream_t)stream;
-  rc = launch_mass<1>(p, (int)D, dtype, shape.waves, s);
-  if (rc) return rc;
-  rc = launch_mass<2>(p, (int)D, dtype, shape.waves, s);
-  if (rc) return rc;
+  const int64_t scratch = single_pass_scratch_bytes(B, Hq, Qb);
+  if (scratch <= kSinglePassScratchMax && workspace_bytes >= spruce_teacher_workspace_bytes(B, Hq, T)) {
+    // [part: B*Hq*2*Qb*Qb floats][rowj: scratch bytes], rowj 256-byte aligned.
+    p.part = workspace;
+    const size_t part_bytes = ((size_t)B * Hq * 2 * Qb * Qb * sizeof(float) + 255) / 256 * 256;
+    p.rowj = reinterpret_cast<float2*>(reinterpret_cast<char*>(workspace) + part_bytes);
+    rc = launch_mass<3>(p, (int)D, dtype, shape.waves, s);
+    if (rc) return rc;
+  } else {
+    p.stats = workspace;
+    p.part = workspace + (size_t)B * Hq * T * 2;
+    rc = launch_mass<1>(p, (int)D, dtype, shape.waves, s);
+    if (rc) return rc;
+    rc = launch_mass<2>(p, (int)D, dtype, shape.waves, s);
+    if (rc) return rc;
+  }
   const int64_t total = B * Hq * Qb * Qb;
   hipLaunchKernelGGL(mass_combine_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, p.part, B * Hq,
                      (int)Qb, mass);
   return check_launch("mass_combine_kernel");
 }
 
-extern "C" size_t spruce_teacher_workspace_bytes(int64_t B, int64_t Hq, int64_t T) {
+extern "C" size_t spruce_teacher_workspace_bytes_min(int64_t B, int64_t Hq, int64_t T) {
   const int64_t Qb = (T + kBlock - 1) / kBlock;
   return (size_t)(B * Hq * T * 2 + B * Hq * 2 * Qb * Qb) * sizeof(float);
+}
+
+extern "C" size_t spruce_teacher_workspace_bytes(int64_t B, int64_t Hq, int64_t T) {
+  const int64_t Qb = (T + kBlock - 1) / kBlock;
+  const int64_t scratch = single_pass_scratch_bytes(B, Hq, Qb);
+  if (scratch <= kSinglePassScratchMax)
+    return ((size_t)B * Hq * 2 * Qb * Qb * sizeof(float) + 255) / 256 * 256 + (size_t)scratch;
+  return spruce_teacher_workspace_bytes_min(B, Hq, T);
 }
 
 extern "C" int spruce_teacher_targets(const float* mass, int64_t B, int64_t Hq, int64_t Hkv, int64_t Qb, int64_t Kb,

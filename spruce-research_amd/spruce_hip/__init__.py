@@ -95,8 +95,9 @@ def lib():
             fn.restype = ctypes.c_int
         handle.spruce_version.restype = ctypes.c_char_p
         handle.spruce_version.argtypes = []
-        handle.spruce_teacher_workspace_bytes.restype = ctypes.c_size_t
-        handle.spruce_teacher_workspace_bytes.argtypes = [_i64, _i64, _i64]
+        for name in ("spruce_teacher_workspace_bytes", "spruce_teacher_workspace_bytes_min"):
+            getattr(handle, name).restype = ctypes.c_size_t
+            getattr(handle, name).argtypes = [_i64, _i64, _i64]
         handle.spruce_kv_summary_workspace_bytes.restype = ctypes.c_size_t
         handle.spruce_kv_summary_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64]
         _lib = handle

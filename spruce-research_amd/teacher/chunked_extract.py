@@ -6,9 +6,12 @@ Drop-in for chunked_pool (teacher/chunked_extract.py:91-131 in the reference):
 pool_attention(causal_softmax(q k^T * scaling)).  ``key`` may be repeated to H
 heads as the reference passes it, or stay at native KV resolution
 ``[b, Hkv, k, d]`` (query head h reads KV head h // (H / Hkv)) -- no GQA copy
-is needed.  Two HIP passes (row statistics, then tile mass) behind the C ABI;
-``head_chunk`` is accepted for signature compatibility and ignored (nothing
-is materialised per head).
+is needed.  One HIP kernel computes QK^T once per causal tile (online row
+statistics plus per-row partial sums in a scratch workspace, combined once
+each row is complete); sequences whose scratch would exceed 4 GiB use two
+passes (row statistics, then recomputed tile mass).  ``head_chunk`` is
+accepted for signature compatibility and ignored (nothing is materialised
+per head).
 
 Selector prototype features (teacher/chunked_extract.py:27-80 in the
 reference), in the model dtype: ``_group_avg_tokens(x, G)`` and
@@ -31,6 +34,14 @@ _PROTO = 8
 @torch.no_grad()
 def chunked_pool(query, key, scaling, block_size=_BLOCK, head_chunk=None):
     del head_chunk
+    return block_mass(query, key, scaling, block_size=block_size)
+
+
+def block_mass(query, key, scaling, block_size=_BLOCK, schedule="auto"):
+    """chunked_pool's computation; ``schedule`` "auto" (single pass when its
+    scratch fits), or "two_pass" (the minimal workspace)."""
+    if schedule not in ("auto", "two_pass"):
+        raise ValueError(f"schedule must be 'auto' or 'two_pass', got {schedule!r}")
     if block_size != _BLOCK:
         raise ValueError("the HIP block-mass kernel requires block_size=64")
     if not query.is_cuda:
@@ -47,7 +58,9 @@ def chunked_pool(query, key, scaling, block_size=_BLOCK, head_chunk=None):
     Hkv = key.shape[1]
     qb = (q_len + _BLOCK - 1) // _BLOCK
     mass = torch.empty((b, H, qb, qb), device=query.device, dtype=torch.float32)
-    nbytes = spruce_hip.lib().spruce_teacher_workspace_bytes(b, H, q_len)
+    size_fn = (spruce_hip.lib().spruce_teacher_workspace_bytes if schedule == "auto"
+               else spruce_hip.lib().spruce_teacher_workspace_bytes_min)
+    nbytes = size_fn(b, H, q_len)
     ws = torch.empty(nbytes // 4, device=query.device, dtype=torch.float32)
     with torch.cuda.device(query.device):
         rc = spruce_hip.lib().spruce_teacher_block_mass(

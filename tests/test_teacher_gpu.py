@@ -14,7 +14,7 @@ import torch
 
 import oracle.teacher as ot
 from spruce_hip import workloads
-from teacher.chunked_extract import chunked_pool
+from teacher.chunked_extract import block_mass, chunked_pool
 from teacher.targets import teacher_targets
 
 pytestmark = pytest.mark.gpu
@@ -41,13 +41,18 @@ def test_block_mass_matches_oracle(H, Hkv, T, D, dtype, repeat):
     q = torch.randn(1, T, H, D, generator=gen).to(dtype).transpose(1, 2)
     k = torch.randn(1, Hkv, T, D, generator=gen).to(dtype)
     kk = k.repeat_interleave(H // Hkv, dim=1) if repeat else k
-    mass = chunked_pool(q.transpose(1, 2).contiguous().to(DEV).transpose(1, 2), kk.to(DEV), D ** -0.5)
     exp = ot.block_mass(q.float().numpy(), kk.float().numpy())
-    _check(mass, exp, f"mass H{H} Hkv{Hkv} T{T} D{D}")
     rows = np.full(exp.shape[2], 64.0)
     rows[-1] = T - 64 * (exp.shape[2] - 1)
-    np.testing.assert_allclose(mass.sum(-1).cpu().numpy(), np.broadcast_to(rows, mass.shape[:3]), rtol=1e-4)
-    assert torch.all(torch.triu(mass, diagonal=1) == 0)
+    qd = q.transpose(1, 2).contiguous().to(DEV).transpose(1, 2)
+    # chunked_pool takes the single pass at these sizes; the two-pass schedule
+    # (the minimal workspace) must agree with the same oracle.
+    for name, mass in (("single", chunked_pool(qd, kk.to(DEV), D ** -0.5)),
+                       ("two_pass", block_mass(qd, kk.to(DEV), D ** -0.5, schedule="two_pass"))):
+        _check(mass, exp, f"mass {name} H{H} Hkv{Hkv} T{T} D{D}")
+        np.testing.assert_allclose(mass.sum(-1).cpu().numpy(), np.broadcast_to(rows, mass.shape[:3]),
+                                   rtol=1e-4)
+        assert torch.all(torch.triu(mass, diagonal=1) == 0)
 
 
 def test_targets_and_topk():
@@ -94,3 +99,9 @@ def test_full_size_cfg4_invariants_and_sampled_rows():
         assert d.max() <= MAX_ABS and d.mean() <= MEAN_ABS
     out = teacher_targets(mass, 4, k=8)
     torch.testing.assert_close(out["target"].sum(-1), torch.ones(1, 4, 256, device=DEV), rtol=1e-4, atol=1e-4)
+    # The two schedules agree everywhere (size-independent cross-check).
+    two = block_mass(q.transpose(1, 2).contiguous().to(DEV).transpose(1, 2), k.to(DEV), 128 ** -0.5,
+                     schedule="two_pass")
+    d = (two - mass).abs()
+    print(f"cfg4 single vs two-pass: max_abs={d.max().item():.3e} mean_abs={d.mean().item():.3e}", flush=True)
+    assert d.max().item() <= 1e-4
