@@ -170,6 +170,35 @@ def main():
             "nnz_kv_blocks": nnz, "flop": flops5,
             "row_blocks_mean": round(float(counts.mean()), 2), "row_blocks_max": int(counts.max()),
         }
+        # Tree route producer at the cfg5 grid (deployed settings of the
+        # reference's export script: radix 2, beam 16, local window 1,
+        # k_selected = beam + 2): prototype features of Q and K, the key tree,
+        # projections, beam traversal and packing into selected_blocks.
+        if not args.no_extra:
+            import math
+            from interfaces.packing import selected_ids_to_blocks
+            from selector.gate import FlatGate
+            from selector.traversal import traverse_to_leaf_ids
+            from selector.tree import build_key_tree
+            from teacher.chunked_extract import _proto_pool_seq, proto_pool_grouped
+            kb5, beam = T5 // 64, 16
+            gate = FlatGate(1, D, proj_dim=D).to(dev).eval()
+
+            def route():
+                qf = proto_pool_grouped(q5, Hkv, 64, 8)
+                kf = _proto_pool_seq(k5, 64, 8)
+                levels = build_key_tree(kf, radix=2)
+                ids = traverse_to_leaf_ids(gate, qf, levels, beam, radix=2)
+                return selected_ids_to_blocks(ids, beam + 2, local_window=1, key_blocks=kb5)
+
+            _, krms = _time_launches(route, max(5, args.steps // 5), max(2, args.warmup // 5))
+            mr = statistics.median(krms)
+            configs["cfg5_tree_route"] = {
+                "ms_median": round(mr, 4), "ms_min": round(min(krms), 4), "ms_max": round(max(krms), 4),
+                "key_blocks": kb5, "kv_groups": Hkv, "prototypes": 8, "proj_dim": D, "beam": beam,
+                "radix": 2, "k_selected": beam + 2,
+                "stages": "proto features (Q group-avg + K) -> build_key_tree -> project -> traverse -> pack",
+            }
         del q5, k5, v5
 
     # ---- cfg3: selector front end, T=65536 (1024 key blocks), top-32

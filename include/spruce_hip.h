@@ -218,6 +218,51 @@ int spruce_gate_scores(const float* qp, const float* kp, int64_t S, int64_t Qb, 
 int spruce_causal_topk(const float* scores, int64_t R, int64_t Qb, int64_t Kb, int64_t k, int32_t* out,
                        void* stream);
 
+/*
+ * One parent level of the key-axis prototype tree.  Replaces
+ * _merge_level_prototypes inside build_key_tree (selector/tree.py:79-145).
+ *   child  [S, n, P, D] contiguous, S = layers * KV groups, dtype bf16/f16/f32.
+ *   parent [S, ceil(n/radix), P, D] contiguous, same dtype.
+ * Parent j covers children [j*radix, min((j+1)*radix, n)).  Prototype 0 is
+ * rnd(rnd(sum of the children's prototype 0) / count) (float32 sum in child
+ * order, rnd = round to the model dtype); prototypes 1..P-1 are the child
+ * prototypes farthest from it in float32 squared L2, farthest first, ties to
+ * the lower candidate (child-major, prototype-minor).  radix*P <= 64, D <= 256.
+ */
+int spruce_tree_merge_level(const void* child, int64_t S, int64_t n, int64_t P, int64_t D, int64_t radix,
+                            int dtype, void* parent, void* stream);
+
+/*
+ * Top-down beam traversal of the key tree.  Replaces traverse_to_leaf_ids
+ * (scripts/eval_tree_traversal.py:59-113).
+ *   qp  [S, qb, Pq, p] float32: projected query prototypes (FlatGate.project_queries).
+ *   kp  [S, N, Pk, p] float32: projected key prototypes of every tree node,
+ *       node IDs leaf-first (level v node i at sum of the lower level counts
+ *       + i; level counts kb, ceil(kb/radix), ..., 1).
+ *   out [S, qb, C] int32 leaf block IDs, score descending (ties to the lower
+ *       node), -1 where no valid candidate was left; C must equal the final
+ *       beam width min over levels of (beam, width*radix, level nodes).
+ * At each level the children of the beam are scored with the MaxSim of
+ * spruce_gate_candidate_scores; a child is valid when it exists and its first
+ * leaf is <= the query block.  beam*radix <= 64, Pq <= 16, Pk <= 64,
+ * p % 4 == 0 and Pq*p <= 8192.  Node choices are bit-reproducible.
+ */
+int spruce_tree_traverse(const float* qp, const float* kp, int64_t S, int64_t qb, int64_t kb, int64_t Pq,
+                         int64_t Pk, int64_t p, int64_t radix, int64_t beam, float div, int32_t* out, int64_t C,
+                         void* stream);
+
+/*
+ * MaxSim scores of per-row candidate nodes.  Replaces
+ * FlatGate.score_projected_candidates (selector/gate.py:129-166).
+ *   qp [S, qb, Pq, p], kp [S, N, Pk, p] float32; ids [S, qb, C] int32
+ *   (clamped to [0, N-1] as the reference does); out [S, qb, C] float32 =
+ *   max over key prototypes c of (max over query prototypes a of the fmaf
+ *   chain q_a . k_c over p), divided by div.
+ */
+int spruce_gate_candidate_scores(const float* qp, const float* kp, const int32_t* ids, int64_t S, int64_t qb,
+                                 int64_t N, int64_t C, int64_t Pq, int64_t Pk, int64_t p, float div, float* out,
+                                 void* stream);
+
 /* ------------------------------------------------------------------------
  * Teacher target extraction.
  * ---------------------------------------------------------------------- */

@@ -1,0 +1,385 @@
+// Tree selector on gfx950: the key-axis prototype tree and its top-down beam
+// traversal, the deployed route producer.
+//
+//   tree_merge_kernel     one parent level of build_key_tree
+//                         (selector/tree.py:79-145, _merge_level_prototypes)
+//   tree_traverse_kernel  traverse_to_leaf_ids
+//                         (scripts/eval_tree_traversal.py:59-113)
+//   candidate_scores_kernel FlatGate.score_projected_candidates
+//                         (selector/gate.py:129-166)
+//
+// Every float is produced by a fixed IEEE single-precision operation
+// sequence (this file is built without contraction, with IEEE division and
+// denormals), so node choices are reproducible bit for bit by a CPU
+// restatement:
+//   merge:  prototype 0 of parent j = rnd(rnd(sum_c x_c) / n) over its n
+//           valid children's prototype 0 (sum from 0.0f, children in order;
+//           rnd = round to the model dtype, as the reference's model-dtype
+//           sum and division do); prototypes 1..P-1 = the P-1 child
+//           prototypes farthest from it in float32 squared L2 (dims summed in
+//           order from 0.0f), farthest first, ties to the lower candidate
+//           index (child-major, prototype-minor), NaN farthest.
+//   score:  for key prototype c, the max over query prototypes a (a
+//           ascending, strict >) of the fmaf chain over the projection dim
+//           from 0.0f; then the max over c (c ascending, strict >); divided
+//           by `div` (= fl(sqrt(p))).
+//   beam:   per level the k = min(beam, candidates, level nodes) valid
+//           candidates with the largest score, ties to the lower node index,
+//           score-descending; missing slots are -1 (the reference ranks
+//           invalid candidates at finfo.min after every valid one).
+#include "common.h"
+
+namespace spruce {
+
+namespace {
+
+constexpr int kMaxLevels = 40;
+
+__device__ __forceinline__ float model_round(float x, int dtype) {
+  if (dtype == SPRUCE_DTYPE_BF16) return (float)(__bf16)x;
+  if (dtype == SPRUCE_DTYPE_F16) return (float)(_Float16)x;
+  return x;
+}
+
+__device__ __forceinline__ float load_elem(const void* base, int64_t i, int dtype) {
+  if (dtype == SPRUCE_DTYPE_F32) return static_cast<const float*>(base)[i];
+  const uint16_t b = static_cast<const uint16_t*>(base)[i];
+  return dtype == SPRUCE_DTYPE_F16 ? unpack1<true>(b) : unpack1<false>(b);
+}
+
+__device__ __forceinline__ void store_elem(void* base, int64_t i, float v, int dtype) {
+  if (dtype == SPRUCE_DTYPE_F32) {
+    static_cast<float*>(base)[i] = v;
+  } else if (dtype == SPRUCE_DTYPE_F16) {
+    static_cast<_Float16*>(base)[i] = (_Float16)v;
+  } else {
+    static_cast<__bf16*>(base)[i] = (__bf16)v;
+  }
+}
+
+// a ranks before b: larger value first, NaN largest, ties to the lower index.
+__device__ __forceinline__ bool ranks_before(float a, int ia, float b, int ib) {
+  const bool na = a != a, nb = b != b;
+  if (na != nb) return na;
+  if (!na && a != b) return a > b;
+  return ia < ib;
+}
+
+struct MergeParams {
+  const void* child;  // [S, n, P, D]
+  void* parent;       // [S, m, P, D]
+  int64_t S;
+  int n, m, P, D, radix, dtype;
+};
+
+// One wavefront per (slab, parent node).
+__global__ __launch_bounds__(64) void tree_merge_kernel(const MergeParams p) {
+  extern __shared__ float sh[];
+  const int64_t g = blockIdx.x;
+  const int64_t s = g / p.m;
+  const int j = (int)(g - s * p.m);
+  if (s >= p.S) return;
+  const int lane = threadIdx.x;
+  const int c0 = j * p.radix;
+  const int cn = p.n - c0 < p.radix ? p.n - c0 : p.radix;  // valid children
+  const int ncand = cn * p.P;
+  const int D = p.D;
+  float* feat = sh;                   // [ncand, D]
+  float* mean = feat + ncand * D;     // [D]
+  float* dist = mean + D;             // [64]
+  const int64_t cbase = ((s * p.n + c0) * p.P) * (int64_t)D;
+  for (int i = lane; i < ncand * D; i += 64) feat[i] = load_elem(p.child, cbase + i, p.dtype);
+  __syncthreads();
+  for (int d = lane; d < D; d += 64) {
+    float acc = 0.f;
+    for (int c = 0; c < cn; ++c) acc = acc + feat[(c * p.P) * D + d];
+    mean[d] = model_round(model_round(acc, p.dtype) / (float)cn, p.dtype);
+  }
+  __syncthreads();
+  if (lane < ncand) {
+    float acc = 0.f;
+    const float* x = feat + lane * D;
+    for (int d = 0; d < D; ++d) {
+      const float df = x[d] - mean[d];
+      acc = acc + df * df;
+    }
+    dist[lane] = acc;
+  }
+  __syncthreads();
+  const int64_t pbase = (s * p.m + j) * (int64_t)p.P * D;
+  for (int d = lane; d < D; d += 64) store_elem(p.parent, pbase + d, mean[d], p.dtype);
+  if (p.P > 1) {
+    int rank = 64;
+    if (lane < ncand) {
+      rank = 0;
+      const float mine = dist[lane];
+      for (int o = 0; o < ncand; ++o) rank += ranks_before(dist[o], o, mine, lane) ? 1 : 0;
+    }
+    // Each selected candidate's lane writes its vector to slot 1 + rank.
+    for (int src = 0; src < ncand; ++src) {
+      const int r = __shfl(rank, src);
+      if (r < p.P - 1)
+        for (int d = lane; d < D; d += 64)
+          store_elem(p.parent, pbase + (int64_t)(1 + r) * D + d, feat[src * D + d], p.dtype);
+    }
+  }
+}
+
+struct ScoreParams2 {
+  const float* qp;  // [S, qb, Pq, p]
+  const float* kp;  // [S, N, Pk, p]
+  int64_t S;
+  int qb, N, Pq, Pk, pd;
+  float div;
+};
+
+// Max over query prototypes of q_a . k (fmaf chains over the projection dim,
+// all a at once; each chain runs e = 0..p-1 in order).  qrow in LDS.
+__device__ __forceinline__ float maxsim_one(const float* qrow, const float* krow, int Pq, int pd) {
+  float acc[16];
+#pragma unroll
+  for (int a = 0; a < 16; ++a) acc[a] = 0.f;
+  for (int e = 0; e < pd; e += 4) {
+    const float4 k4 = *reinterpret_cast<const float4*>(krow + e);
+#pragma unroll
+    for (int a = 0; a < 16; ++a) {
+      if (a < Pq) {
+        const float4 q4 = *reinterpret_cast<const float4*>(qrow + a * pd + e);
+        float t = acc[a];
+        t = fmaf(q4.x, k4.x, t);
+        t = fmaf(q4.y, k4.y, t);
+        t = fmaf(q4.z, k4.z, t);
+        t = fmaf(q4.w, k4.w, t);
+        acc[a] = t;
+      }
+    }
+  }
+  float best = acc[0];
+#pragma unroll
+  for (int a = 1; a < 16; ++a)
+    if (a < Pq && acc[a] > best) best = acc[a];
+  return best;
+}
+
+struct TraverseParams {
+  ScoreParams2 sc;
+  int kb, radix, beam, levels, C;
+  int count[kMaxLevels];
+  int offset[kMaxLevels];
+  int64_t span[kMaxLevels];  // leaves per node at each level (radix^v)
+  int32_t* out;              // [S, qb, C]
+};
+
+// One wavefront per (slab, query block) row.
+__global__ __launch_bounds__(64) void tree_traverse_kernel(const TraverseParams p) {
+  extern __shared__ float sh[];
+  const ScoreParams2& sc = p.sc;
+  const int64_t row = blockIdx.x;
+  const int64_t s = row / sc.qb;
+  const int q = (int)(row - s * sc.qb);
+  if (s >= sc.S) return;
+  const int lane = threadIdx.x;
+  float* qrow = sh;                          // [Pq, p]
+  float* pm = qrow + sc.Pq * sc.pd;          // [64, Pk] per-(candidate, key prototype) max
+  float* score = pm + 64 * sc.Pk;            // [64]
+  int* cand = reinterpret_cast<int*>(score + 64);   // [64]
+  int* valid = cand + 64;                    // [64]
+  int* sel = valid + 64;                     // [64] current beam (node index within level)
+  const float* qsrc = sc.qp + (s * sc.qb + q) * (int64_t)sc.Pq * sc.pd;
+  for (int i = lane; i < sc.Pq * sc.pd; i += 64) qrow[i] = qsrc[i];
+  if (lane == 0) sel[0] = 0;  // the root
+  int W = 1;
+  __syncthreads();
+  for (int v = p.levels - 2; v >= 0; --v) {
+    const int ncand = W * p.radix;
+    if (lane < ncand) {
+      const int par = sel[lane / p.radix];
+      const int c = par >= 0 ? par * p.radix + lane % p.radix : -1;
+      const bool ok = par >= 0 && c < p.count[v] && (int64_t)c * p.span[v] <= q;
+      cand[lane] = c;
+      valid[lane] = ok ? 1 : 0;
+    }
+    __syncthreads();
+    const float* kl = sc.kp + (s * sc.N + p.offset[v]) * (int64_t)sc.Pk * sc.pd;
+    for (int pr = lane; pr < ncand * sc.Pk; pr += 64) {
+      const int i = pr / sc.Pk, c = pr - (pr / sc.Pk) * sc.Pk;
+      float m = 0.f;
+      if (valid[i]) m = maxsim_one(qrow, kl + ((int64_t)cand[i] * sc.Pk + c) * sc.pd, sc.Pq, sc.pd);
+      pm[i * sc.Pk + c] = m;
+    }
+    __syncthreads();
+    if (lane < ncand) {
+      float best = pm[lane * sc.Pk];
+      for (int c = 1; c < sc.Pk; ++c)
+        if (pm[lane * sc.Pk + c] > best) best = pm[lane * sc.Pk + c];
+      score[lane] = best / sc.div;
+    }
+    __syncthreads();
+    int k = p.beam < ncand ? p.beam : ncand;
+    k = k < p.count[v] ? k : p.count[v];
+    int rank = 64;
+    if (lane < ncand) {
+      const bool mine_ok = valid[lane] != 0;
+      rank = 0;
+      for (int o = 0; o < ncand; ++o) {
+        if (o == lane) continue;
+        const bool ook = valid[o] != 0;
+        bool before;
+        if (ook != mine_ok) before = ook;                 // valid candidates rank first
+        else if (!ook) before = o < lane;                  // invalid: any fixed order
+        else before = ranks_before(score[o], cand[o], score[lane], cand[lane]);
+        rank += before ? 1 : 0;
+      }
+    }
+    __syncthreads();
+    if (lane < ncand && rank < k) sel[rank] = valid[lane] ? cand[lane] : -1;
+    W = k;
+    __syncthreads();
+  }
+  int32_t* o = p.out + row * (int64_t)p.C;
+  for (int i = lane; i < p.C; i += 64) o[i] = i < W ? sel[i] : -1;
+}
+
+struct CandParams {
+  ScoreParams2 sc;
+  const int32_t* ids;  // [S, qb, C]
+  int C;
+  float* out;          // [S, qb, C]
+};
+
+// One wavefront per (slab, query block) row; lanes over (candidate, key prototype).
+__global__ __launch_bounds__(64) void candidate_scores_kernel(const CandParams p) {
+  extern __shared__ float sh[];
+  const ScoreParams2& sc = p.sc;
+  const int64_t row = blockIdx.x;
+  const int64_t s = row / sc.qb;
+  if (s >= sc.S) return;
+  const int lane = threadIdx.x;
+  float* qrow = sh;
+  float* pm = qrow + sc.Pq * sc.pd;  // [64, Pk]
+  const float* qsrc = sc.qp + row * (int64_t)sc.Pq * sc.pd;
+  for (int i = lane; i < sc.Pq * sc.pd; i += 64) qrow[i] = qsrc[i];
+  __syncthreads();
+  const int32_t* idr = p.ids + row * (int64_t)p.C;
+  for (int c0 = 0; c0 < p.C; c0 += 64) {
+    const int nc = p.C - c0 < 64 ? p.C - c0 : 64;
+    for (int pr = lane; pr < nc * sc.Pk; pr += 64) {
+      const int i = pr / sc.Pk, c = pr - (pr / sc.Pk) * sc.Pk;
+      int node = idr[c0 + i];
+      node = node < 0 ? 0 : (node >= sc.N ? sc.N - 1 : node);  // clamped like the reference
+      pm[i * sc.Pk + c] = maxsim_one(qrow, sc.kp + ((s * sc.N + node) * sc.Pk + c) * (int64_t)sc.pd, sc.Pq, sc.pd);
+    }
+    __syncthreads();
+    if (lane < nc) {
+      float best = pm[lane * sc.Pk];
+      for (int c = 1; c < sc.Pk; ++c)
+        if (pm[lane * sc.Pk + c] > best) best = pm[lane * sc.Pk + c];
+      p.out[row * (int64_t)p.C + c0 + lane] = best / sc.div;
+    }
+    __syncthreads();
+  }
+}
+
+int check_score_args(const float* qp, const float* kp, int64_t S, int64_t qb, int64_t N, int64_t Pq, int64_t Pk,
+                     int64_t pd, float div) {
+  SPRUCE_REQUIRE(qp && kp, "projected query and key pointers must be non-null");
+  SPRUCE_REQUIRE(S >= 1 && qb >= 1 && N >= 1, "S, qb and N must be positive");
+  SPRUCE_REQUIRE(Pq >= 1 && Pq <= 16, "query prototypes must be in [1, 16], got %lld", (long long)Pq);
+  SPRUCE_REQUIRE(Pk >= 1 && Pk <= 64, "key prototypes must be in [1, 64], got %lld", (long long)Pk);
+  SPRUCE_REQUIRE(pd >= 4 && pd % 4 == 0 && Pq * pd <= 8192, "projection dim must be a multiple of 4 with Pq*p <= 8192");
+  SPRUCE_REQUIRE(((uintptr_t)qp % 16) == 0 && ((uintptr_t)kp % 16) == 0, "projections must be 16-byte aligned");
+  SPRUCE_REQUIRE(div > 0.f, "div must be positive");
+  SPRUCE_REQUIRE(S * qb < ((int64_t)1 << 31), "too many rows");
+  return SPRUCE_OK;
+}
+
+}  // namespace
+}  // namespace spruce
+
+using namespace spruce;
+
+extern "C" int spruce_tree_merge_level(const void* child, int64_t S, int64_t n, int64_t P, int64_t D, int64_t radix,
+                                       int dtype, void* parent, void* stream) {
+  SPRUCE_REQUIRE(child && parent, "child and parent must be non-null device pointers");
+  SPRUCE_REQUIRE(S >= 1 && n >= 1 && P >= 1 && D >= 1, "S, n, P and D must be positive");
+  SPRUCE_REQUIRE(radix >= 2, "radix must be >= 2, got %lld", (long long)radix);
+  SPRUCE_REQUIRE(radix * P <= 64, "radix * P must be <= 64, got %lld", (long long)(radix * P));
+  SPRUCE_REQUIRE(D <= 256, "feature dim must be <= 256, got %lld", (long long)D);
+  SPRUCE_REQUIRE(dtype == SPRUCE_DTYPE_BF16 || dtype == SPRUCE_DTYPE_F16 || dtype == SPRUCE_DTYPE_F32,
+                 "unsupported dtype code %d", dtype);
+  MergeParams p{};
+  p.child = child;
+  p.parent = parent;
+  p.S = S;
+  p.n = (int)n;
+  p.m = (int)((n + radix - 1) / radix);
+  p.P = (int)P;
+  p.D = (int)D;
+  p.radix = (int)radix;
+  p.dtype = dtype;
+  SPRUCE_REQUIRE(S * p.m < ((int64_t)1 << 31), "too many parent nodes");
+  const size_t lds = ((size_t)radix * P * D + D + 64) * sizeof(float);
+  SPRUCE_REQUIRE(lds <= 65536, "radix * P * D too large for one workgroup's LDS (%zu bytes)", lds);
+  hipLaunchKernelGGL(tree_merge_kernel, dim3((unsigned)(S * p.m)), dim3(64), lds, (hipStream_t)stream, p);
+  return check_launch("tree_merge_kernel");
+}
+
+extern "C" int spruce_tree_traverse(const float* qp, const float* kp, int64_t S, int64_t qb, int64_t kb, int64_t Pq,
+                                    int64_t Pk, int64_t pd, int64_t radix, int64_t beam, float div, int32_t* out,
+                                    int64_t C, void* stream) {
+  SPRUCE_REQUIRE(out != nullptr, "out must be a non-null device pointer");
+  SPRUCE_REQUIRE(kb >= 1 && kb < ((int64_t)1 << 30), "key blocks must be in [1, 2^30)");
+  SPRUCE_REQUIRE(radix >= 2, "radix must be >= 2, got %lld", (long long)radix);
+  SPRUCE_REQUIRE(beam >= 1, "beam must be >= 1, got %lld", (long long)beam);
+  SPRUCE_REQUIRE(beam * radix <= 64, "beam * radix must be <= 64, got %lld", (long long)(beam * radix));
+  TraverseParams p{};
+  // Level counts ceil(prev / radix) down to one root; node (v, i) has ID offset[v] + i.
+  int64_t count = kb, span = 1, total = 0;
+  int levels = 0;
+  while (true) {
+    SPRUCE_REQUIRE(levels < kMaxLevels, "tree too deep");
+    p.count[levels] = (int)count;
+    p.offset[levels] = (int)total;
+    p.span[levels] = span;
+    total += count;
+    ++levels;
+    if (count == 1) break;
+    count = (count + radix - 1) / radix;
+    span *= radix;
+  }
+  int rc = check_score_args(qp, kp, S, qb, total, Pq, Pk, pd, div);
+  if (rc) return rc;
+  // Output width: the beam width after the last level.
+  int64_t W = 1;
+  for (int v = levels - 2; v >= 0; --v) {
+    int64_t k = beam < W * radix ? beam : W * radix;
+    W = k < p.count[v] ? k : p.count[v];
+  }
+  SPRUCE_REQUIRE(C == W, "out width must be %lld for this tree and beam, got %lld", (long long)W, (long long)C);
+  p.sc = ScoreParams2{qp, kp, S, (int)qb, (int)total, (int)Pq, (int)Pk, (int)pd, div};
+  p.kb = (int)kb;
+  p.radix = (int)radix;
+  p.beam = (int)beam;
+  p.levels = levels;
+  p.C = (int)C;
+  p.out = out;
+  const size_t lds = ((size_t)Pq * pd + 64 * Pk + 64) * sizeof(float) + 3 * 64 * sizeof(int);
+  hipLaunchKernelGGL(tree_traverse_kernel, dim3((unsigned)(S * qb)), dim3(64), lds, (hipStream_t)stream, p);
+  return check_launch("tree_traverse_kernel");
+}
+
+extern "C" int spruce_gate_candidate_scores(const float* qp, const float* kp, const int32_t* ids, int64_t S,
+                                            int64_t qb, int64_t N, int64_t C, int64_t Pq, int64_t Pk, int64_t pd,
+                                            float div, float* out, void* stream) {
+  int rc = check_score_args(qp, kp, S, qb, N, Pq, Pk, pd, div);
+  if (rc) return rc;
+  SPRUCE_REQUIRE(C >= 1 && ids != nullptr && out != nullptr, "ids and out must be non-null with C >= 1");
+  CandParams p{};
+  p.sc = ScoreParams2{qp, kp, S, (int)qb, (int)N, (int)Pq, (int)Pk, (int)pd, div};
+  p.ids = ids;
+  p.C = (int)C;
+  p.out = out;
+  const size_t lds = ((size_t)Pq * pd + 64 * Pk) * sizeof(float);
+  hipLaunchKernelGGL(candidate_scores_kernel, dim3((unsigned)(S * qb)), dim3(64), lds, (hipStream_t)stream, p);
+  return check_launch("candidate_scores_kernel");
+}

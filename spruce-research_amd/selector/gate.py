@@ -4,7 +4,9 @@ Drop-in for the reference's ``FlatGate`` (selector/gate.py:16-175) on the
 scoring path: the same constructor, parameters (``Wq``, ``Wk`` of shape
 ``[L, d, p]``, kaiming-uniform like nn.Linear) and
 ``forward(q_feat [L,G,qb,P,d], k_feat [L,G,kb,P,d]) -> [L,G,qb,kb]``
-MaxSim scores divided by sqrt(p).  Projection and scoring run as HIP kernels.
+MaxSim scores divided by sqrt(p), and the traversal's candidate scoring
+(``score_projected_candidates``, ``score_candidates``).  Projection and
+scoring run as HIP kernels.
 Training (autograd through the scores) stays with the reference: this module
 scores only, and raises if asked for gradients.
 """
@@ -13,6 +15,7 @@ import math
 import torch
 import torch.nn as nn
 
+import spruce_hip
 from selector.select import gate_scores, project
 
 
@@ -40,6 +43,42 @@ class FlatGate(nn.Module):
     def project_keys(self, k_feat):
         """[L,G,kb,P,d] -> [L,G,kb,P,p] (selector/gate.py:124-127)."""
         return torch.stack([project(k_feat[l].float(), self.Wk[l].float()) for l in range(k_feat.shape[0])])
+
+    @torch.no_grad()
+    def score_projected_candidates(self, projected_q, projected_k, candidate_ids, layer_chunk=1):
+        """Scores ``[L,G,qb,C]`` of per-row candidate node IDs ``[L,G,qb,C]``
+        (clamped to the node range) against projected prototypes
+        (selector/gate.py:129-166); one HIP launch, no gathered candidates."""
+        if projected_q.dim() != 5 or projected_k.dim() != 5 or candidate_ids.dim() != 4:
+            raise ValueError("candidate scoring expects q/k 5-D and IDs 4-D")
+        L, G, qb = projected_q.shape[:3]
+        if projected_k.shape[:2] != (L, G) or candidate_ids.shape[:3] != (L, G, qb):
+            raise ValueError("candidate scoring layer/group/query dimensions mismatch")
+        if layer_chunk < 1:
+            raise ValueError("layer_chunk must be >= 1")
+        if not projected_q.is_cuda:
+            raise RuntimeError("the HIP FlatGate requires GPU tensors")
+        qp = projected_q.float().contiguous()
+        kp = projected_k.float().contiguous()
+        ids = candidate_ids.to(torch.int32).contiguous()
+        N, Pk, p = kp.shape[2:]
+        C = ids.shape[-1]
+        out = torch.empty((L, G, qb, C), device=qp.device, dtype=torch.float32)
+        if C == 0:
+            return out
+        with torch.cuda.device(qp.device):
+            rc = spruce_hip.lib().spruce_gate_candidate_scores(
+                spruce_hip.ptr(qp), spruce_hip.ptr(kp), spruce_hip.ptr(ids), L * G, qb, N, C,
+                qp.shape[3], Pk, p, float(math.sqrt(self.proj_dim)), spruce_hip.ptr(out),
+                spruce_hip.stream_of(qp))
+        spruce_hip.check(rc, "spruce_gate_candidate_scores")
+        return out
+
+    @torch.no_grad()
+    def score_candidates(self, q_feat, k_feat, candidate_ids):
+        """Projects Q/K once, then scores the candidates (selector/gate.py:168-172)."""
+        return self.score_projected_candidates(
+            self.project_queries(q_feat), self.project_keys(k_feat), candidate_ids)
 
     def forward(self, q_feat, k_feat, causal=False):
         """Raw MaxSim scores ``[L,G,qb,kb]`` / sqrt(p); ``causal`` sets j > i to -inf."""
