@@ -139,8 +139,11 @@ __device__ __forceinline__ float maxsim_one(const float* qrow, const float* krow
   float acc[16];
 #pragma unroll
   for (int a = 0; a < 16; ++a) acc[a] = 0.f;
+  // The key vector streams from L2 one 64-byte line quarter ahead of its use.
+  float4 knext = *reinterpret_cast<const float4*>(krow);
   for (int e = 0; e < pd; e += 4) {
-    const float4 k4 = *reinterpret_cast<const float4*>(krow + e);
+    const float4 k4 = knext;
+    if (e + 4 < pd) knext = *reinterpret_cast<const float4*>(krow + e + 4);
 #pragma unroll
     for (int a = 0; a < 16; ++a) {
       if (a < Pq) {
