@@ -171,13 +171,24 @@ struct BlockIter<kModeCsr> {
   }
 };
 
+// Mask rows are scanned 64 columns at a time with ballots; the bytes of the
+// next 64 columns are loaded one chunk ahead and kept raw, so the wait for
+// them falls where they are used (behind any key block loads issued later).
+constexpr int kMaxUnion = 5;  // query heads the tiles of one workgroup (<= 8 waves) can span
+
 template <>
 struct BlockIter<kModeMask> {
   const uint8_t* base;  // row of the first head of the union
-  const uint8_t* own;   // row of this wave's head
   int64_t hstride, cstride;
-  int nunion, qb, chunk, lane;
+  int nunion, own, qb, chunk, lane;
   uint64_t bits, ownbits;
+  uint32_t raw[kMaxUnion];  // prefetched bytes of chunk `chunk` for this lane's column
+  __device__ void fetch() {
+    const int col = chunk * 64 + lane;
+#pragma unroll
+    for (int h = 0; h < kMaxUnion; ++h)
+      raw[h] = (h < nunion && col <= qb) ? base[(int64_t)h * hstride + (int64_t)col * cstride] : 0u;
+  }
   __device__ void init(const AttnParams& p, int b, int g, int qb_, int part, int hq, int lane_) {
     cstride = p.ms[3];
     qb = qb_;
@@ -194,29 +205,30 @@ struct BlockIter<kModeMask> {
       base = p.mask + (int64_t)b * p.ms[0] + (int64_t)(g * p.G + h0) * p.ms[1] + (int64_t)qb_ * p.ms[2];
       hstride = p.ms[1];
       nunion = h1 - h0 + 1;
-      int oh = hq - h0;
-      if (oh < 0) oh = 0;
-      if (oh >= nunion) oh = nunion - 1;
-      own = base + (int64_t)oh * hstride;
+      own = hq - h0;
+      if (own < 0) own = 0;
+      if (own >= nunion) own = nunion - 1;
     } else {
       base = p.mask + (int64_t)b * p.ms[0] + (int64_t)g * p.ms[1] + (int64_t)qb_ * p.ms[2];
       hstride = 0;
       nunion = 1;
-      own = base;
+      own = 0;
     }
+    fetch();
   }
   __device__ bool next(int& id, bool& en) {
     while (bits == 0) {
       if (chunk * 64 > qb) return false;
-      const int col = chunk * 64 + lane;
       bool u = false, o = false;
-      if (col <= qb) {
-        for (int h = 0; h < nunion; ++h) u |= base[(int64_t)h * hstride + (int64_t)col * cstride] != 0;
-        o = own[(int64_t)col * cstride] != 0;
+#pragma unroll
+      for (int h = 0; h < kMaxUnion; ++h) {
+        u |= raw[h] != 0u;
+        o |= (h == own) && raw[h] != 0u;
       }
       bits = __ballot(u);
       ownbits = __ballot(o);
       ++chunk;
+      fetch();
     }
     const int pz = __builtin_ctzll(bits);
     bits &= bits - 1;
@@ -351,6 +363,7 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
 
   // ---- Q fragment (B operand of S^T = K Q^T), resident for the whole row
   uint4 qf[KS];
+  raw8_t<TIn> qraw[KS];
   {
     const int64_t qrs = p.qs[2] * EB;
     int nq = p.T - q0;
@@ -361,9 +374,24 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
         (uint32_t)(nq * qrs));
     const int vq = l32 * (int)qrs + 8 * hl * EB;
 #pragma unroll
-    for (int kk = 0; kk < KS; ++kk)
-      qf[kk] = to_mfma_scaled<TIn, F16>(buf_load8<TIn>(rq, vq + 16 * kk * EB), p.qmul, p.prescale != 0);
+    for (int kk = 0; kk < KS; ++kk) qraw[kk] = buf_load8<TIn>(rq, vq + 16 * kk * EB);
   }
+  // The fragments are converted (prescaled, or rounded from fp32) only once
+  // the first key block's loads are in flight, so the Q and K/V round trips
+  // overlap instead of running back to back.
+  bool q_ready = false;
+  auto convert_q = [&]() {
+    q_ready = true;
+    if (p.prescale) {
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) qf[kk] = to_mfma_scaled<TIn, F16>(qraw[kk], p.qmul, true);
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) qf[kk] = raw_to_mfma<TIn, F16>(qraw[kk]);
+    }
+  };
+  // The summary form converts at once: its registers are tighter.
+  if constexpr (SUMM) convert_q();
 
   // ---- per-lane staging offsets, constant across blocks
   const char* kbase = static_cast<const char*>(p.k) + ((int64_t)b * p.ks[0] + (int64_t)g * p.ks[1]) * EB;
@@ -537,6 +565,7 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
   int buf = 0;
   if (it.next(cur_id, cur_en)) {
     load_block(cur_id);
+    if (!q_ready) convert_q();
     store_block(0);
     __syncthreads();
     while (true) {
@@ -569,6 +598,7 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
       if (m) nn = j0 + 64 - __builtin_clzll(m);
     }
     const int E = nn * p.P;
+    if (E > 0 && !q_ready) convert_q();  // the row listed no exact block
     const int64_t bg = (int64_t)b * p.Hkv + g;
     auto node_of = [&](int en) {
       if (en >= E) return -1;
@@ -611,6 +641,47 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     }
   }
 
+  if constexpr (EB == 2) {
+    // The output tile goes through LDS so that every store writes whole
+    // 16-byte pieces of 256-byte rows (the accumulator layout would write 8
+    // bytes to each of 64 rows per instruction).  The K/V tiles are free
+    // once every wave is past its last block.
+    constexpr int OSTR = D + 8;
+    static_assert(WAVES * 32 * OSTR <= 2 * BUF, "output staging must fit the K/V tiles");
+    __syncthreads();
+    if (!active) return;
+    const float lt = l_run + __shfl_xor(l_run, 32);
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    uint16_t* ot = smem + wave * 32 * OSTR;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int d = dt * 32 + 8 * j + 4 * hl;
+        const uint32_t w0 = pack2<F16>(acc[dt][4 * j] * inv, acc[dt][4 * j + 1] * inv);
+        const uint32_t w1 = pack2<F16>(acc[dt][4 * j + 2] * inv, acc[dt][4 * j + 3] * inv);
+        *reinterpret_cast<uint2*>(ot + l32 * OSTR + d) = uint2{w0, w1};
+      }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int64_t ors = p.os[2] * EB;
+    int nq = p.T - q0;
+    nq = nq < 0 ? 0 : (nq > 32 ? 32 : nq);
+    const __amdgpu_buffer_rsrc_t ro = make_rsrc(
+        static_cast<char*>(p.o) + ((int64_t)b * p.os[0] + (int64_t)head * p.os[1] + (int64_t)q0 * p.os[2]) * EB,
+        (uint32_t)(nq * ors));
+    constexpr int CH = D / 8;  // 16-byte pieces per row
+#pragma unroll
+    for (int i = 0; i < 32 * CH / 64; ++i) {
+      const int c = i * 64 + lane;
+      const int row = c / CH, ch = c % CH;
+      const uint4 v = *reinterpret_cast<const uint4*>(ot + row * OSTR + ch * 8);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int, v),
+                                             ro, row * (int)ors + ch * 16, 0, 0);
+    }
+    return;
+  }
   if (!active) return;
   const float lt = l_run + __shfl_xor(l_run, 32);
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
