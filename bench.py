@@ -201,6 +201,29 @@ def main():
             }
         del q5, k5, v5
 
+    # ---- capture pass: dense causal cfg2 layer that also emits the selector
+    # features (group-averaged Q, key prototypes; the Q prototypes pooled by
+    # one small launch), against the same work done in separate passes.
+    if not args.no_extra:
+        from teacher.chunked_extract import _proto_pool_seq, causal_prefill_features, proto_pool_grouped
+        fnc = lambda: causal_prefill_features(q, k, v, scale, 8)  # noqa: E731
+        fnu = lambda: (causal_prefill_features(q, k, v, scale, capture=False),  # noqa: E731
+                       proto_pool_grouped(q, Hkv, 64, 8), _proto_pool_seq(k, 64, 8))
+        _, kums = _time_launches(fnu, max(5, args.steps // 5), max(2, args.warmup // 5))
+        _, kcms = _time_launches(fnc, max(5, args.steps // 5), max(2, args.warmup // 5))
+        mc, mu = statistics.median(kcms), statistics.median(kums)
+        qbk = T // 64
+        flc = qbk * (qbk + 1) // 2 * Hq * BLOCK_FLOPS
+        configs["cfg2_capture_32k"] = {
+            "ms_median": round(mc, 4), "ms_min": round(min(kcms), 4), "ms_max": round(max(kcms), 4),
+            "tflops": round(flc / (mc * 1e-3) / 1e12, 2),
+            "frac_bf16_peak": round(flc / (mc * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "flop": flc, "prototypes": 8,
+            "separate_passes_ms_median": round(mu, 4),
+            "stages": "dense causal attention + group-averaged Q + key prototypes in one pass, "
+                      "then Q prototypes pooled from the grouped tokens",
+        }
+
     # ---- cfg3: selector front end, T=65536 (1024 key blocks), top-32
     if not args.no_extra:
         from selector.select import select_blocks

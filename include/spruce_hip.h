@@ -80,6 +80,34 @@ int spruce_sparse_prefill_index(
     void* stream);
 
 /*
+ * Dense causal GQA prefill: every key block 0..qb of every query block, in
+ * order (the all-causal-blocks case of the entry points above), with the
+ * same q/k/v/out layouts and limits.  Replaces the fused causal SDPA call of
+ * the reference's capture hooks (teacher/chunked_extract.py:155-161,
+ * :175-181); out written through its strides, e.g. [B, T, Hq, D] as the hooks
+ * return it.
+ * With q_grouped and k_protos non-NULL the same pass also emits the
+ * selector features of those hooks (:145-148, :170-173) from the tiles it
+ * holds:
+ *   q_grouped [B, Hkv, T, D] contiguous: _group_avg_tokens (:75-80) of q;
+ *   k_protos  [B, Hkv, ceil(T/64), P, D] contiguous: _proto_pool_seq(k, 64,
+ *             P) (:27-72);
+ * bit for bit equal to spruce_group_avg_tokens / spruce_proto_pool.  Capture
+ * needs dtype bf16 or f16, Hq/Hkv <= 8, 1 <= P <= 65 and 16-byte aligned
+ * q_grouped / k_protos; pooling q_grouped with spruce_proto_pool (G == H)
+ * gives the query prototypes.
+ */
+int spruce_causal_prefill(
+    const void* q, const int64_t qs[4],
+    const void* k, const int64_t ks[4],
+    const void* v, const int64_t vs[4],
+    int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D,
+    float scale, int dtype,
+    void* out, const int64_t os[4],
+    void* q_grouped, void* k_protos, int64_t P,
+    void* stream);
+
+/*
  * Same computation over a CSR list (variable row lengths).  Rows are the
  * (b, kv_head, query_block) triples in row-major order; row r lists
  * indices[indptr[r] .. indptr[r+1]).  indptr has B*Hkv*ceil(T/64)+1 int32

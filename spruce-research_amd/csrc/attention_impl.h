@@ -27,6 +27,12 @@
 //     block;
 //   * skipped blocks are never touched: the block list is walked once and only
 //     listed blocks are loaded.
+//
+// The dense causal form (every block 0..qb, in order) can also emit the
+// selector features of the reference's capture hooks
+// (teacher/chunked_extract.py:27-80,163-180) from the tiles it already holds:
+// the group-averaged query tokens from each wave's resident Q fragment and the
+// key prototypes of block qb from the diagonal K tile left in LDS.
 #pragma once
 
 #include <type_traits>
@@ -37,7 +43,7 @@ namespace spruce {
 
 constexpr int kBlock = 64;
 
-enum : int { kModePadded = 0, kModeCsr = 1, kModeMask = 2 };
+enum : int { kModePadded = 0, kModeCsr = 1, kModeMask = 2, kModeCausal = 3 };
 
 struct AttnParams {
   const void* q;
@@ -72,6 +78,14 @@ struct AttnParams {
   const float* sval;
   const float* slog;
   float sbias;  // log counts -> raw score units: log2(e) / cs
+  // feature capture (dense causal form): group-averaged queries
+  // [B, Hkv, T, D] and key prototypes [B, Hkv, Qb, P, D], model dtype,
+  // contiguous.  tpp = tiles per part; each part covers tpp / G whole
+  // 32-row halves of the query block.
+  void* qgrp;
+  void* kproto;
+  int tpp;
+  float inv_rep;
 };
 
 struct F32x8 {
@@ -168,6 +182,22 @@ struct BlockIter<kModeCsr> {
       }
     }
     return false;
+  }
+};
+
+// Dense causal: every key block 0..qb, in order (the diagonal block last).
+template <>
+struct BlockIter<kModeCausal> {
+  int pos, qb;
+  __device__ void init(const AttnParams&, int, int, int qb_, int, int, int) {
+    pos = 0;
+    qb = qb_;
+  }
+  __device__ bool next(int& id, bool& en) {
+    if (pos > qb) return false;
+    id = pos++;
+    en = true;
+    return true;
   }
 };
 
@@ -299,14 +329,125 @@ __device__ __forceinline__ void store_vt4(uint16_t* dst, int vstride, const uint
   }
 }
 
+// ------------------------------------------------------------ feature capture
+// Arithmetic of the selector features (the same operation sequences as the
+// standalone prototype kernels, so the results agree bit for bit; no FP
+// contraction here):
+//   key prototypes of a block: prototype 0 = rnd(rnd(sum_t k_t) / n) over the
+//     block's n real rows (rows summed in order from 0.0f; the reference sums
+//     and divides in the model dtype, teacher/chunked_extract.py:46-47);
+//     prototypes 1..k, k = min(P-1, 64), are the k rows farthest from it in
+//     float32 squared L2 (dims in order from 0.0f), farthest first, ties to
+//     the lower row, NaN largest (:55-58); slots without a real row hold the
+//     mean (:65-72).
+//   group-averaged queries: rnd(sum_h q_h * fl(1/G)) over the G query heads of
+//     the KV head, heads in order from 0.0f (torch's mean, :75-80); G == 1
+//     copies the row.
+// rnd() rounds to the model dtype.
+template <bool F16>
+__device__ __forceinline__ float model_rnd(float x) {
+  if constexpr (F16) return (float)(_Float16)x;
+  else return (float)(__bf16)x;
+}
+
+// Ks: the block's K tile in LDS (row stride KSTR, raw model-dtype bits);
+// scratch: >= (D + 64) * 4 bytes of LDS no other wave touches; n: real rows.
+// Called by every thread of the workgroup (it contains barriers).
+template <int D, int KSTR, int NTHR, bool F16>
+__device__ void capture_key_prototypes(const uint16_t* Ks, float* scratch, int n, int P, uint16_t* dst, int tid) {
+#pragma clang fp contract(off)
+  float* mean = scratch;
+  int* pick = reinterpret_cast<int*>(scratch + D);
+  if (tid < D) {
+    float s = 0.0f;
+    for (int t = 0; t < n; ++t) s = s + unpack1<F16>(Ks[t * KSTR + tid]);
+    mean[tid] = model_rnd<F16>(model_rnd<F16>(s) / (float)n);
+  }
+  __syncthreads();
+  const int k = P - 1 < kBlock ? P - 1 : kBlock;
+  if (tid < 64) {
+    // Lane = row of the block; rows past the real ones rank as -inf.
+    float dist = -__builtin_inff();
+    if (tid < n) {
+      float s = 0.0f;
+      for (int d = 0; d < D; ++d) {
+        const float diff = unpack1<F16>(Ks[tid * KSTR + d]) - mean[d];
+        s = s + diff * diff;
+      }
+      dist = s;
+    }
+    // Order key: larger distance first, any NaN above +inf, then lower row.
+    const uint32_t u = __builtin_bit_cast(uint32_t, dist);
+    const uint32_t okey = dist != dist ? 0xffffffffu : ((u & 0x80000000u) ? ~u : (u | 0x80000000u));
+    bool taken = false;
+    for (int j = 0; j < k; ++j) {
+      uint64_t key = taken ? 0ull : (((uint64_t)okey << 32) | (uint32_t)(63 - tid));
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) {
+        const uint64_t o = __shfl_xor(key, m, 64);
+        key = o > key ? o : key;
+      }
+      const int best = 63 - (int)(key & 63u);
+      if (tid == best) taken = true;
+      if (tid == 0) pick[j] = best;
+    }
+  }
+  __syncthreads();
+  constexpr int CH = D / 8;
+  for (int c = tid; c < P * CH; c += NTHR) {
+    const int slot = c / CH, d0 = (c - slot * CH) * 8;
+    const int row = (slot >= 1 && slot <= k) ? pick[slot - 1] : kBlock;
+    uint4 w;
+    if (row < n) {
+      w = *reinterpret_cast<const uint4*>(Ks + row * KSTR + d0);
+    } else {
+      w = uint4{pack2<F16>(mean[d0], mean[d0 + 1]), pack2<F16>(mean[d0 + 2], mean[d0 + 3]),
+                pack2<F16>(mean[d0 + 4], mean[d0 + 5]), pack2<F16>(mean[d0 + 6], mean[d0 + 7])};
+    }
+    *reinterpret_cast<uint4*>(dst + (int64_t)slot * D + d0) = w;
+  }
+}
+
+// qst: slot w = lh * G + h holds the 32 rows of query head h, half lh, of
+// this part (row stride RS, raw model-dtype bits).  Writes the nh * 32
+// group-averaged rows starting at token t_first (rows at or past T skipped).
+template <int D, int NTHR, bool F16>
+__device__ void capture_group_average(const uint16_t* qst, int RS, int G, int nh, float inv_rep, int t_first, int T,
+                                      uint16_t* dst, int tid) {
+#pragma clang fp contract(off)
+  constexpr int CH = D / 8;
+  for (int task = tid; task < nh * 32 * CH; task += NTHR) {
+    const int r = task / CH, c = task - (task / CH) * CH;
+    if (t_first + r >= T) continue;
+    const int lh = r >> 5, rr = r & 31;
+    const uint16_t* src = qst + (lh * G * 32 + rr) * RS + 8 * c;
+    uint4 w = *reinterpret_cast<const uint4*>(src);
+    if (G > 1) {
+      float s[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s[j] = 0.0f + unpack1<F16>(elem16(w, j));
+      for (int h = 1; h < G; ++h) {
+        const uint4 x = *reinterpret_cast<const uint4*>(src + h * 32 * RS);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s[j] = s[j] + unpack1<F16>(elem16(x, j));
+      }
+      w = uint4{pack2<F16>(s[0] * inv_rep, s[1] * inv_rep), pack2<F16>(s[2] * inv_rep, s[3] * inv_rep),
+                pack2<F16>(s[4] * inv_rep, s[5] * inv_rep), pack2<F16>(s[6] * inv_rep, s[7] * inv_rep)};
+    }
+    *reinterpret_cast<uint4*>(dst + (int64_t)r * D + 8 * c) = w;
+  }
+}
+
 // Softmax reference point: the running max is only raised when a row's max
 // grows by more than this (log2 units), so most blocks skip the O rescale.
 // Exponents stay <= 2^8, far inside fp32/bf16/f16 range; the final O / l is
 // unchanged because O and l share the same reference point.
 constexpr float kRescaleThreshold = 8.0f;
 
-template <int D, int WAVES, typename TIn, bool F16, int MODE, bool SUMM = false>
+template <int D, int WAVES, typename TIn, bool F16, int MODE, bool SUMM = false, bool CAP = false>
 __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnParams p) {
+  static_assert(!CAP || (MODE == kModeCausal && !SUMM && TIn::bytes == 2),
+                "feature capture runs on the dense causal form in the model dtype");
   constexpr int NTHR = WAVES * 64;
   constexpr int KSTR = D + 8;        // K tile row stride, 16-bit elements (16 B pad)
   constexpr int VSTR = kBlock + 8;   // V^T tile row stride
@@ -354,12 +495,25 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     b = bg / p.Hkv;
     g = bg - b * p.Hkv;
   }
-  const int tile = part * WAVES + wave;
-  const bool active = tile < 2 * p.G;
-  const int hq = active ? (tile >> 1) : 0;
+  // Tile t of the row is query head t / 2, half t % 2; the capture form
+  // orders them half-major (t = half * G + head) so that each part holds
+  // every query head of its halves for the group average.
+  bool active;
+  int hq, qhalf;
+  if constexpr (CAP) {
+    const int t = part * p.tpp + wave;
+    active = wave < p.tpp;
+    qhalf = active ? t / p.G : 0;
+    hq = active ? t - qhalf * p.G : 0;
+  } else {
+    const int tile = part * WAVES + wave;
+    active = tile < 2 * p.G;
+    hq = active ? (tile >> 1) : 0;
+    qhalf = tile & 1;
+  }
   const int head = g * p.G + hq;
-  const int q0 = qb * kBlock + (tile & 1) * 32;  // first query of this wave's tile
-  const int qin = (tile & 1) * 32 + l32;         // this lane's query row in the block
+  const int q0 = qb * kBlock + qhalf * 32;  // first query of this wave's tile
+  const int qin = qhalf * 32 + l32;         // this lane's query row in the block
 
   // ---- Q fragment (B operand of S^T = K Q^T), resident for the whole row
   uint4 qf[KS];
@@ -641,6 +795,33 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     }
   }
 
+  if constexpr (CAP) {
+    // Every block 0..qb was walked in order, so buffer `buf` still holds the
+    // diagonal K tile and the other buffer has no readers left.
+    constexpr int QRS = D + 8;
+    static_assert(WAVES * 32 * QRS <= 2 * BUF, "query staging must fit the K/V tiles");
+    const int64_t bg = (int64_t)b * p.Hkv + g;
+    if (part == 0) {
+      int n = p.T - qb * kBlock;
+      n = n > kBlock ? kBlock : n;
+      capture_key_prototypes<D, KSTR, NTHR, F16>(smem + buf * BUF, reinterpret_cast<float*>(smem + (buf ^ 1) * BUF),
+                                                 n, p.P,
+                                                 static_cast<uint16_t*>(p.kproto) + (bg * p.Qb + qb) * p.P * D, tid);
+    }
+    __syncthreads();
+    if (active) {
+      // The Q fragments are the raw model-dtype rows (never prescaled here).
+      uint16_t* qd = smem + (wave * 32 + l32) * QRS + 8 * hl;
+#pragma unroll
+      for (int kk = 0; kk < KS; ++kk) *reinterpret_cast<uint4*>(qd + 16 * kk) = qf[kk];
+    }
+    __syncthreads();
+    const int nh = p.tpp / p.G;
+    const int t_first = qb * kBlock + part * nh * 32;
+    capture_group_average<D, NTHR, F16>(smem, QRS, p.G, nh, p.inv_rep, t_first, p.T,
+                                        static_cast<uint16_t*>(p.qgrp) + (bg * p.T + t_first) * D, tid);
+  }
+
   if constexpr (EB == 2) {
     // The output tile goes through LDS so that every store writes whole
     // 16-byte pieces of 256-byte rows (the accumulator layout would write 8
@@ -729,12 +910,12 @@ inline LaunchShape choose_shape(int variant, int G) {
   return {4, (tiles + 3) / 4};
 }
 
-template <int D, int WAVES, typename TIn, bool F16, int MODE, bool SUMM>
+template <int D, int WAVES, typename TIn, bool F16, int MODE, bool SUMM, bool CAP = false>
 int launch_attention_t(const AttnParams& p, hipStream_t stream) {
   // Rows are padded to a multiple of the 8 XCDs; the extra workgroups exit.
   const int64_t rows8 = ((int64_t)p.B * p.Hkv * p.Qb + 7) / 8 * 8;
   const int64_t grid = rows8 * p.parts;
-  hipLaunchKernelGGL((sparse_prefill_kernel<D, WAVES, TIn, F16, MODE, SUMM>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((sparse_prefill_kernel<D, WAVES, TIn, F16, MODE, SUMM, CAP>), dim3((unsigned)grid),
                      dim3(WAVES * 64), 0, stream, p);
   return check_launch("sparse_prefill_kernel");
 }

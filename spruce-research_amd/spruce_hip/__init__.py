@@ -40,6 +40,9 @@ _SIGNATURES = {
         _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _i64,
         _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int, ctypes.c_int,
         _p, _STRIDES, _p],
+    "spruce_causal_prefill": [
+        _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _i64, _i64, _i64, _i64, _i64, ctypes.c_float,
+        ctypes.c_int, _p, _STRIDES, _p, _p, _i64, _p],
     "spruce_sparse_prefill_csr": [
         _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _p, _p, _i64, _p,
         _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int, ctypes.c_int,

@@ -134,12 +134,68 @@ def _group_avg_tokens(x, G):
     return out
 
 
+@torch.no_grad()
+def causal_prefill_features(query, key, value, scaling, P=_PROTO, capture=True):
+    """Dense causal GQA attention of the capture hooks with the selector
+    features as a by-product of the same HIP pass (``spruce_causal_prefill``).
+
+    query ``[b,H,L,d]`` (any strides with a contiguous last dim, e.g. the
+    transposed view of a ``[b,L,H,d]`` projection); key/value ``[b,G,L,d]`` at
+    KV-head resolution (no repeat).  Returns ``(attn_output, pooled_q,
+    pooled_k)``: attn_output ``[b,L,H,d]`` contiguous (what the hooks return,
+    teacher/chunked_extract.py:155-161 in the reference), pooled_q =
+    ``_proto_pool_seq(_group_avg_tokens(query, G), 64, P)`` and pooled_k =
+    ``_proto_pool_seq(key, 64, P)`` (:145-147), bit for bit the standalone
+    kernels' results.  The attention kernel writes the group-averaged query
+    tokens and the key prototypes while it holds the tiles; one small launch
+    pools the grouped queries.  ``capture=False`` runs the attention only
+    (pooled_* are None).
+    """
+    from kernels.direct_index import _check_common, _output
+    B, H, G, L, d = _check_common(query, key, value, _BLOCK, "tiled_gqa")
+    if any(x.stride(-1) != 1 for x in (query, key, value)):
+        raise ValueError("query, key and value must have a contiguous final dimension")
+    q_grouped = k_protos = None
+    if capture:
+        if query.dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError(f"feature capture runs in the model dtype (bf16 or f16), got {query.dtype}")
+        if H // G > 8:
+            raise ValueError(f"feature capture supports at most 8 query heads per KV head, got {H // G}")
+        if not 1 <= P <= 65:
+            raise ValueError(f"P must be in [1, 65], got {P}")
+        nb = (L + _BLOCK - 1) // _BLOCK
+        q_grouped = torch.empty((B, G, L, d), device=query.device, dtype=query.dtype)
+        k_protos = torch.empty((B, G, nb, P, d), device=query.device, dtype=query.dtype)
+    out, out_strides = _output(query)
+    with torch.cuda.device(query.device):
+        rc = spruce_hip.lib().spruce_causal_prefill(
+            spruce_hip.ptr(query), spruce_hip.strides(query), spruce_hip.ptr(key), spruce_hip.strides(key),
+            spruce_hip.ptr(value), spruce_hip.strides(value), B, H, G, L, d, float(scaling),
+            spruce_hip.dtype_code(query), spruce_hip.ptr(out), out_strides,
+            spruce_hip.ptr(q_grouped), spruce_hip.ptr(k_protos), P, spruce_hip.stream_of(query))
+    spruce_hip.check(rc, "spruce_causal_prefill")
+    if not capture:
+        return out, None, None
+    return out, _launch_proto(q_grouped, G, _BLOCK, P), k_protos
+
+
+def _fused_capture_ok(query, key, value, dropout):
+    # The fused pass covers the hooks' deployed settings; anything else keeps
+    # the separate prototype kernels plus torch's fused SDPA, as the reference.
+    return (_BLOCK == 64 and not dropout and query.dtype in (torch.bfloat16, torch.float16)
+            and query.shape[-1] in (64, 128) and query.shape[1] % key.shape[1] == 0
+            and query.shape[1] // key.shape[1] <= 8
+            and query.stride(-1) == 1 and key.stride(-1) == 1 and value.stride(-1) == 1)
+
+
 # ---------------------------------------------------------------------------
 # Hugging Face capture hooks (teacher/chunked_extract.py:134-265 in the reference).
 # The attention function computes the teacher mass (HIP chunked_pool at native
-# KV resolution: no repeated K copy) and the selector prototypes (one fused HIP
-# kernel per side), then propagates the layer through torch's fused causal SDPA
-# as the reference does.
+# KV resolution: no repeated K copy), then propagates the layer through the HIP
+# dense causal kernel, which emits the selector prototypes from the same pass
+# (bf16/f16, head_dim 64/128, at most 8 query heads per KV head, no dropout;
+# other settings keep the standalone prototype kernels and torch's fused causal
+# SDPA, as the reference).
 
 # layer_idx -> pooled mass [1, H, qb, kb] (cpu, float32)
 _CAPTURE = {}
@@ -171,12 +227,20 @@ def _capture_qk(module, query, key):
     _CAPTURE_QK[module.layer_idx] = (pooled_q, pooled_k)
 
 
+def _capture_fused(module, query, key, value, scaling):
+    out, pooled_q, pooled_k = causal_prefill_features(query, key, value, scaling, _PROTO)
+    _CAPTURE_QK[module.layer_idx] = (pooled_q.cpu(), pooled_k.cpu())
+    return out
+
+
 def _capture_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0,
                        sliding_window=None, **kwargs):
     """Attention function "chunked_capture": records mass and prototypes for the layer."""
     if scaling is None:
         scaling = query.shape[-1] ** -0.5
     _CAPTURE[module.layer_idx] = chunked_pool(query, key, scaling, _BLOCK).cpu()
+    if _fused_capture_ok(query, key, value, dropout):
+        return _capture_fused(module, query, key, value, scaling), None
     _capture_qk(module, query, key)
     return _propagate(query, key, value, scaling, dropout), None
 
@@ -186,6 +250,8 @@ def _capture_features(module, query, key, value, attention_mask, scaling=None, d
     """Attention function "selector_feature_capture": prototypes only, no teacher mass."""
     if scaling is None:
         scaling = query.shape[-1] ** -0.5
+    if _fused_capture_ok(query, key, value, dropout):
+        return _capture_fused(module, query, key, value, scaling), None
     _capture_qk(module, query, key)
     return _propagate(query, key, value, scaling, dropout), None
 
