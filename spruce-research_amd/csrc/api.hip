@@ -82,6 +82,7 @@ int prepare_attention(AttnParams& p, const void* q, const int64_t qs[4], const v
   p.qmul = scale * log2e;
   shape = choose_shape(variant, p.G);
   p.parts = shape.parts;
+  p.tpp = shape.tpp;
   const int64_t grid = ((int64_t)B * Hkv * p.Qb + 7) / 8 * 8 * shape.parts;
   SPRUCE_REQUIRE(grid < ((int64_t)1 << 31), "grid too large");
   return SPRUCE_OK;

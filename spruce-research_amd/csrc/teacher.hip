@@ -40,6 +40,7 @@ struct MassParams {
   const void* k;
   int64_t qs[4], ks[4];
   int B, Hq, Hkv, T, G, Qb, parts;
+  int tpp;      // tiles per part: waves 0..tpp-1 own a tile
   float cs;     // scale * log2(e)
   float* stats;  // [B, Hq, T, 2]: (row max in log2 units, row sum), two-pass only
   float* part;   // [B, Hq, 2, Qb, Qb]
@@ -81,8 +82,8 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
   const int qb = p.Qb - 1 - roww / bh;  // heaviest rows first
   const int bg = roww - (roww / bh) * bh;
   const int b = bg / p.Hkv, g = bg - (bg / p.Hkv) * p.Hkv;
-  const int tile = part * WAVES + wave;
-  const bool active = tile < 2 * p.G;
+  const int tile = part * p.tpp + wave;
+  const bool active = wave < p.tpp && tile < 2 * p.G;
   const int hq = active ? (tile >> 1) : 0;
   const int head = g * p.G + hq;
   const int half = tile & 1;
@@ -388,7 +389,6 @@ int launch_mass_w(const MassParams& p, int waves, hipStream_t s) {
   switch (waves) {
     case 2: hipLaunchKernelGGL((block_mass_kernel<D, 2, TIn, F16, PASS>), dim3((unsigned)grid), dim3(128), 0, s, p); break;
     case 4: hipLaunchKernelGGL((block_mass_kernel<D, 4, TIn, F16, PASS>), dim3((unsigned)grid), dim3(256), 0, s, p); break;
-    case 7: hipLaunchKernelGGL((block_mass_kernel<D, 7, TIn, F16, PASS>), dim3((unsigned)grid), dim3(448), 0, s, p); break;
     case 8: hipLaunchKernelGGL((block_mass_kernel<D, 8, TIn, F16, PASS>), dim3((unsigned)grid), dim3(512), 0, s, p); break;
     default: return set_error(SPRUCE_EINVAL, "unsupported wave count %d", waves);
   }
@@ -441,6 +441,7 @@ extern "C" int spruce_teacher_block_mass(const void* q, const int64_t qs[4], con
   p.G = (int)(Hq / Hkv);
   p.Qb = (int)Qb;
   p.parts = shape.parts;
+  p.tpp = shape.tpp;
   p.cs = scale * 1.4426950408889634f;
   hipStream_t s = (hipStream_t)stream;
   const int64_t scratch = single_pass_scratch_bytes(B, Hq, Qb);
