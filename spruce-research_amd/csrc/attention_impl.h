@@ -442,10 +442,11 @@ __device__ void capture_group_average(const uint16_t* qst, int RS, int G, int nh
 // unchanged because O and l share the same reference point.
 constexpr float kRescaleThreshold = 8.0f;
 
-template <int D, int WAVES, typename TIn, bool F16, int MODE, bool SUMM = false, bool CAP = false>
+template <int D, int WAVES, typename TIn, bool F16, int MODE, bool SUMM = false, bool CAP = false, bool PROD = false>
 __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnParams p) {
   static_assert(!CAP || (MODE == kModeCausal && !SUMM && TIn::bytes == 2),
                 "feature capture runs on the dense causal form in the model dtype");
+  static_assert(!PROD || (!SUMM && TIn::bytes == 2), "the producer form stages 16-bit K/V for key blocks only");
   constexpr int NTHR = WAVES * 64;
   constexpr int KSTR = D + 8;        // K tile row stride, 16-bit elements (16 B pad)
   constexpr int VSTR = kBlock + 8;   // V^T tile row stride
@@ -603,6 +604,45 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     }
   };
 
+  // Producer form: the last wave (which owns no tile) stages every K/V block
+  // alone, so the tile waves carry no staging registers or copy work.
+  constexpr int PKCH = KCHUNKS / 64;  // K chunks per producer lane
+  constexpr int PVTK = VTASKS / 64;   // V tasks per producer lane
+  static_assert(KCHUNKS % 64 == 0 && VTASKS % 64 == 0, "producer lanes split the block evenly");
+  auto produce = [&](int blk, int buf) {
+    const int t0 = blk * kBlock;
+    int nk = p.T - t0;
+    nk = nk > kBlock ? kBlock : nk;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + (int64_t)t0 * krs, (uint32_t)(nk * krs));
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + (int64_t)t0 * vrs, (uint32_t)(nk * vrs));
+    raw8_t<TIn> ks8[PKCH];
+    raw8_t<TIn> vs8[PVTK][4];
+#pragma unroll
+    for (int i = 0; i < PKCH; ++i) {
+      const int c = lane + 64 * i;
+      ks8[i] = buf_load8<TIn>(rk, (c / KROWCH) * krs + (c % KROWCH) * 8 * EB);
+    }
+#pragma unroll
+    for (int i = 0; i < PVTK; ++i) {
+      const int t = lane + 64 * i;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) vs8[i][j] = buf_load8<TIn>(rv, (4 * (t & 15) + j) * vrs + (t >> 4) * 8 * EB);
+    }
+    uint16_t* Ks = smem + buf * BUF;
+    uint16_t* Vt = Ks + KTILE;
+#pragma unroll
+    for (int i = 0; i < PKCH; ++i) {
+      const int c = lane + 64 * i;
+      *reinterpret_cast<uint4*>(Ks + (c / KROWCH) * KSTR + (c % KROWCH) * 8) = raw_to_mfma<TIn, F16>(ks8[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < PVTK; ++i) {
+      const int t = lane + 64 * i;
+      store_vt4(Vt + 8 * (t >> 4) * VSTR + vt_pos(4 * (t & 15)), VSTR, raw_to_mfma<TIn, F16>(vs8[i][0]),
+                raw_to_mfma<TIn, F16>(vs8[i][1]), raw_to_mfma<TIn, F16>(vs8[i][2]), raw_to_mfma<TIn, F16>(vs8[i][3]));
+    }
+  };
+
   float m_use = -INFINITY;  // softmax reference point (scaled, log2 domain)
   float l_run = 0.f;        // running sum over this lane half's keys
   f32x16_t acc[DT];
@@ -716,22 +756,53 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
   bool cur_en = false;
   int buf = 0;
   if (it.next(cur_id, cur_en)) {
-    load_block(cur_id);
-    if (!q_ready) convert_q();
-    store_block(0);
-    __syncthreads();
-    while (true) {
-      int nid = 0;
-      bool nen = false;
-      const bool more = it.next(nid, nen);
-      if (more) load_block(nid);
-      if (active && cur_en) compute(buf, cur_id == qb, nullptr);
-      if (!more) break;
-      store_block(buf ^ 1);
+    if constexpr (PROD) {
+      // Same barrier sequence on both sides: one before the first block and
+      // one between consecutive blocks.
+      if (wave == WAVES - 1) {
+        produce(cur_id, 0);
+        __syncthreads();
+        while (true) {
+          int nid = 0;
+          bool nen = false;
+          if (!it.next(nid, nen)) break;
+          produce(nid, buf ^ 1);
+          __syncthreads();
+          buf ^= 1;
+        }
+      } else {
+        if (!q_ready) convert_q();
+        __syncthreads();
+        while (true) {
+          int nid = 0;
+          bool nen = false;
+          const bool more = it.next(nid, nen);
+          if (active && cur_en) compute(buf, cur_id == qb, nullptr);
+          if (!more) break;
+          __syncthreads();
+          buf ^= 1;
+          cur_id = nid;
+          cur_en = nen;
+        }
+      }
+    } else {
+      load_block(cur_id);
+      if (!q_ready) convert_q();
+      store_block(0);
       __syncthreads();
-      buf ^= 1;
-      cur_id = nid;
-      cur_en = nen;
+      while (true) {
+        int nid = 0;
+        bool nen = false;
+        const bool more = it.next(nid, nen);
+        if (more) load_block(nid);
+        if (active && cur_en) compute(buf, cur_id == qb, nullptr);
+        if (!more) break;
+        store_block(buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
+        cur_id = nid;
+        cur_en = nen;
+      }
     }
   }
 
@@ -891,6 +962,8 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
 }
 
 // ------------------------------------------------------------------ launch
+constexpr bool kUseProducer = true;
+
 struct LaunchShape {
   int waves;
   int parts;
@@ -913,12 +986,12 @@ inline LaunchShape choose_shape(int variant, int G) {
   return tiles % 4 == 0 ? LaunchShape{4, tiles / 4, 4} : LaunchShape{2, tiles / 2, 2};
 }
 
-template <int D, int WAVES, typename TIn, bool F16, int MODE, bool SUMM, bool CAP = false>
+template <int D, int WAVES, typename TIn, bool F16, int MODE, bool SUMM, bool CAP = false, bool PROD = false>
 int launch_attention_t(const AttnParams& p, hipStream_t stream) {
   // Rows are padded to a multiple of the 8 XCDs; the extra workgroups exit.
   const int64_t rows8 = ((int64_t)p.B * p.Hkv * p.Qb + 7) / 8 * 8;
   const int64_t grid = rows8 * p.parts;
-  hipLaunchKernelGGL((sparse_prefill_kernel<D, WAVES, TIn, F16, MODE, SUMM, CAP>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((sparse_prefill_kernel<D, WAVES, TIn, F16, MODE, SUMM, CAP, PROD>), dim3((unsigned)grid),
                      dim3(WAVES * 64), 0, stream, p);
   return check_launch("sparse_prefill_kernel");
 }
@@ -928,7 +1001,11 @@ int launch_attention_w(const AttnParams& p, int waves, hipStream_t stream) {
   switch (waves) {
     case 2: return launch_attention_t<D, 2, TIn, F16, MODE, SUMM>(p, stream);
     case 4: return launch_attention_t<D, 4, TIn, F16, MODE, SUMM>(p, stream);
-    case 8: return launch_attention_t<D, 8, TIn, F16, MODE, SUMM>(p, stream);
+    case 8:
+      // A spare wave becomes the K/V producer (16-bit inputs, key blocks only).
+      if constexpr (kUseProducer && TIn::bytes == 2 && !SUMM)
+        if (p.tpp < 8) return launch_attention_t<D, 8, TIn, F16, MODE, SUMM, false, true>(p, stream);
+      return launch_attention_t<D, 8, TIn, F16, MODE, SUMM>(p, stream);
     default: return set_error(SPRUCE_EINVAL, "unsupported wave count %d", waves);
   }
 }

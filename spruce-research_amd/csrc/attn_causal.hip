@@ -11,6 +11,7 @@ namespace {
 
 template <int D, typename TIn, bool F16>
 int launch_capture(const AttnParams& p, hipStream_t stream) {
+  if (p.tpp < 8) return launch_attention_t<D, 8, TIn, F16, kModeCausal, false, true, kUseProducer>(p, stream);
   return launch_attention_t<D, 8, TIn, F16, kModeCausal, false, true>(p, stream);
 }
 
