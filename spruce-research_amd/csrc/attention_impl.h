@@ -609,14 +609,14 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
   constexpr int PKCH = KCHUNKS / 64;  // K chunks per producer lane
   constexpr int PVTK = VTASKS / 64;   // V tasks per producer lane
   static_assert(KCHUNKS % 64 == 0 && VTASKS % 64 == 0, "producer lanes split the block evenly");
-  auto produce = [&](int blk, int buf) {
+  raw8_t<TIn> ks8[PKCH];
+  raw8_t<TIn> vs8[PVTK][4];
+  auto pload = [&](int blk) {
     const int t0 = blk * kBlock;
     int nk = p.T - t0;
     nk = nk > kBlock ? kBlock : nk;
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + (int64_t)t0 * krs, (uint32_t)(nk * krs));
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + (int64_t)t0 * vrs, (uint32_t)(nk * vrs));
-    raw8_t<TIn> ks8[PKCH];
-    raw8_t<TIn> vs8[PVTK][4];
 #pragma unroll
     for (int i = 0; i < PKCH; ++i) {
       const int c = lane + 64 * i;
@@ -628,6 +628,8 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
 #pragma unroll
       for (int j = 0; j < 4; ++j) vs8[i][j] = buf_load8<TIn>(rv, (4 * (t & 15) + j) * vrs + (t >> 4) * 8 * EB);
     }
+  };
+  auto pstore = [&](int buf) {
     uint16_t* Ks = smem + buf * BUF;
     uint16_t* Vt = Ks + KTILE;
 #pragma unroll
@@ -642,6 +644,10 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
                 raw_to_mfma<TIn, F16>(vs8[i][1]), raw_to_mfma<TIn, F16>(vs8[i][2]), raw_to_mfma<TIn, F16>(vs8[i][3]));
     }
   };
+  auto produce = [&](int blk, int buf) {
+    pload(blk);
+    pstore(buf);
+  };
 
   float m_use = -INFINITY;  // softmax reference point (scaled, log2 domain)
   float l_run = 0.f;        // running sum over this lane half's keys
@@ -649,12 +655,12 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16_t{};
 
-  // sb: per-key score bias of a summary chunk (null for a key block).
-  auto compute = [&](int buf, bool diag, const float* sb) {
-    const uint16_t* Ks = smem + buf * BUF;
-    const uint16_t* Vt = Ks + KTILE;
-    // S^T (64 keys x 32 queries) as two 32x32 tiles, LDS reads one k-step ahead.
-    f32x16_t s0 = f32x16_t{}, s1 = f32x16_t{};
+  // The block step in three pieces: S^T = K Q^T into (sc0, sc1); the online
+  // softmax of those scores into the packed P fragments pk (and the O and
+  // l rescale); O^T += V^T P^T.
+  f32x16_t sc0, sc1;
+  uint4 pk[2][2];
+  auto scores = [&](const uint16_t* Ks) {
     const uint16_t* kp = Ks + l32 * KSTR + 8 * hl;
     // All K fragments of the block are read before the first MFMA (pinned by
     // the scheduling barrier), so the matrix cores never wait on a just-issued
@@ -666,11 +672,18 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
       a1[kk] = *reinterpret_cast<const uint4*>(kp + 32 * KSTR + 16 * kk);
     }
     __builtin_amdgcn_sched_barrier(0);
+    f32x16_t s0 = f32x16_t{}, s1 = f32x16_t{};
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
       s0 = mfma32x32x16<F16>(a0[kk], qf[kk], s0);
       s1 = mfma32x32x16<F16>(a1[kk], qf[kk], s1);
     }
+    sc0 = s0;
+    sc1 = s1;
+  };
+  // sb: per-key score bias of a summary chunk (null for a key block).
+  auto softmax = [&](bool diag, const float* sb) {
+    f32x16_t s0 = sc0, s1 = sc1;
     if (diag) {
       // Register r of key tile c holds key 32c + 8(r/4) + 4(lane/32) + r%4.
       const int thr = qin - 4 * hl;
@@ -714,7 +727,6 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     // m_use = -inf; exp2(-inf) = 0 needs a finite offset there.
     const float nm = (sb != nullptr && m_use == -INFINITY) ? 0.f : -m_use;
     float psum = 0.f;
-    uint4 pk[2][2];
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2) {
       uint32_t w0[4], w1[4];
@@ -732,9 +744,11 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
       pk[1][h2] = uint4{w1[0], w1[1], w1[2], w1[3]};
     }
     l_run += psum;
-    // O^T += V^T P^T, V^T fragments one step ahead.
-    // Same for the V^T fragments; consecutive MFMAs go to different output
-    // tiles (dt fastest), so no MFMA waits on the previous one's result.
+  };
+  // O^T += V^T P^T.  All V^T fragments are read first, as for K;
+  // consecutive MFMAs go to different output tiles (dt fastest), so no MFMA
+  // waits on the previous one's result.
+  auto pv = [&](const uint16_t* Vt) {
     const uint16_t* vp = Vt + l32 * VSTR + 8 * hl;
     uint4 va[DT * 4];
 #pragma unroll
@@ -748,6 +762,12 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
       const int dt = i % DT, ch = i / DT, c = ch >> 1, h2 = ch & 1;
       acc[dt] = mfma32x32x16<F16>(va[i], pk[c][h2], acc[dt]);
     }
+  };
+  auto compute = [&](int buf, bool diag, const float* sb) {
+    const uint16_t* Ks = smem + buf * BUF;
+    scores(Ks);
+    softmax(diag, sb);
+    pv(Ks + KTILE);
   };
 
   BlockIter<MODE> it;

@@ -164,6 +164,72 @@ __device__ __forceinline__ float maxsim_one(const float* qrow, const float* krow
   return best;
 }
 
+// Two (candidate, key prototype) pairs per lane against a compile-time
+// number of query prototypes: every query float4 read from LDS feeds both
+// pairs, and each chain is the same fmaf sequence as maxsim_one (e
+// ascending), so the results are identical.  The key vectors stream in
+// 64-byte pieces (4 float4 loads back to back, the next piece in flight
+// while the current one is used): lanes read different vectors, and taking
+// a line in two pieces close together keeps it in L1 between them, where
+// one float4 per step was refetched from L2 for every 16 bytes (measured
+// 1.85 -> 1.0-1.1 ms at the cfg5 grid).  Requires pd % 16 == 0.
+template <int PQ>
+__device__ __forceinline__ void maxsim_pair(const float* qrow, const float* ka, const float* kb, int pd, float& ra,
+                                            float& rb) {
+  constexpr int CW = 4;  // float4 per piece
+  float acc0[PQ], acc1[PQ];
+#pragma unroll
+  for (int a = 0; a < PQ; ++a) acc0[a] = acc1[a] = 0.f;
+  float4 na[CW], nb[CW];
+#pragma unroll
+  for (int j = 0; j < CW; ++j) {
+    na[j] = *reinterpret_cast<const float4*>(ka + 4 * j);
+    nb[j] = *reinterpret_cast<const float4*>(kb + 4 * j);
+  }
+  for (int e0 = 0; e0 < pd; e0 += 4 * CW) {
+    float4 ca[CW], cb[CW];
+#pragma unroll
+    for (int j = 0; j < CW; ++j) {
+      ca[j] = na[j];
+      cb[j] = nb[j];
+    }
+    if (e0 + 4 * CW < pd) {
+#pragma unroll
+      for (int j = 0; j < CW; ++j) {
+        na[j] = *reinterpret_cast<const float4*>(ka + e0 + 4 * CW + 4 * j);
+        nb[j] = *reinterpret_cast<const float4*>(kb + e0 + 4 * CW + 4 * j);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < CW; ++j) {
+      const int e = e0 + 4 * j;
+#pragma unroll
+      for (int a = 0; a < PQ; ++a) {
+        const float4 q4 = *reinterpret_cast<const float4*>(qrow + a * pd + e);
+        float t = acc0[a], u = acc1[a];
+        t = fmaf(q4.x, ca[j].x, t);
+        u = fmaf(q4.x, cb[j].x, u);
+        t = fmaf(q4.y, ca[j].y, t);
+        u = fmaf(q4.y, cb[j].y, u);
+        t = fmaf(q4.z, ca[j].z, t);
+        u = fmaf(q4.z, cb[j].z, u);
+        t = fmaf(q4.w, ca[j].w, t);
+        u = fmaf(q4.w, cb[j].w, u);
+        acc0[a] = t;
+        acc1[a] = u;
+      }
+    }
+  }
+  float x = acc0[0], y = acc1[0];
+#pragma unroll
+  for (int a = 1; a < PQ; ++a) {
+    if (acc0[a] > x) x = acc0[a];
+    if (acc1[a] > y) y = acc1[a];
+  }
+  ra = x;
+  rb = y;
+}
+
 struct TraverseParams {
   ScoreParams2 sc;
   int kb, radix, beam, levels, C;
@@ -173,7 +239,9 @@ struct TraverseParams {
   int32_t* out;              // [S, qb, C]
 };
 
-// One wavefront per (slab, query block) row.
+// One wavefront per (slab, query block) row.  PQ > 0: that many query
+// prototypes, two pairs per lane per step; PQ == 0: any count, one pair.
+template <int PQ>
 __global__ __launch_bounds__(64) void tree_traverse_kernel(const TraverseParams p) {
   extern __shared__ float sh[];
   const ScoreParams2& sc = p.sc;
@@ -204,11 +272,29 @@ __global__ __launch_bounds__(64) void tree_traverse_kernel(const TraverseParams 
     }
     __syncthreads();
     const float* kl = sc.kp + (s * sc.N + p.offset[v]) * (int64_t)sc.Pk * sc.pd;
-    for (int pr = lane; pr < ncand * sc.Pk; pr += 64) {
-      const int i = pr / sc.Pk, c = pr - (pr / sc.Pk) * sc.Pk;
-      float m = 0.f;
-      if (valid[i]) m = maxsim_one(qrow, kl + ((int64_t)cand[i] * sc.Pk + c) * sc.pd, sc.Pq, sc.pd);
-      pm[i * sc.Pk + c] = m;
+    const int npairs = ncand * sc.Pk;
+    if (PQ > 0 && sc.pd % 16 == 0) {
+      // Pairs pr and pr + 64; an invalid or missing pair reads the level's
+      // first node (always in range) and its result is dropped.
+      for (int pr = lane; pr < npairs; pr += 128) {
+        const int pr2 = pr + 64;
+        const int i0 = pr / sc.Pk, c0 = pr - i0 * sc.Pk;
+        const int i1 = pr2 < npairs ? pr2 / sc.Pk : 0, c1 = pr2 < npairs ? pr2 - i1 * sc.Pk : 0;
+        const bool v0 = valid[i0] != 0, v1 = pr2 < npairs && valid[i1] != 0;
+        const float* k0 = kl + (v0 ? ((int64_t)cand[i0] * sc.Pk + c0) * sc.pd : 0);
+        const float* k1 = kl + (v1 ? ((int64_t)cand[i1] * sc.Pk + c1) * sc.pd : 0);
+        float m0, m1;
+        maxsim_pair<PQ == 0 ? 1 : PQ>(qrow, k0, k1, sc.pd, m0, m1);
+        pm[i0 * sc.Pk + c0] = v0 ? m0 : 0.f;
+        if (pr2 < npairs) pm[i1 * sc.Pk + c1] = v1 ? m1 : 0.f;
+      }
+    } else {
+      for (int pr = lane; pr < npairs; pr += 64) {
+        const int i = pr / sc.Pk, c = pr - (pr / sc.Pk) * sc.Pk;
+        float m = 0.f;
+        if (valid[i]) m = maxsim_one(qrow, kl + ((int64_t)cand[i] * sc.Pk + c) * sc.pd, sc.Pq, sc.pd);
+        pm[i * sc.Pk + c] = m;
+      }
     }
     __syncthreads();
     if (lane < ncand) {
@@ -367,7 +453,14 @@ extern "C" int spruce_tree_traverse(const float* qp, const float* kp, int64_t S,
   p.C = (int)C;
   p.out = out;
   const size_t lds = ((size_t)Pq * pd + 64 * Pk + 64) * sizeof(float) + 3 * 64 * sizeof(int);
-  hipLaunchKernelGGL(tree_traverse_kernel, dim3((unsigned)(S * qb)), dim3(64), lds, (hipStream_t)stream, p);
+  const dim3 grid((unsigned)(S * qb));
+  switch (Pq) {
+    case 1: hipLaunchKernelGGL(tree_traverse_kernel<1>, grid, dim3(64), lds, (hipStream_t)stream, p); break;
+    case 2: hipLaunchKernelGGL(tree_traverse_kernel<2>, grid, dim3(64), lds, (hipStream_t)stream, p); break;
+    case 4: hipLaunchKernelGGL(tree_traverse_kernel<4>, grid, dim3(64), lds, (hipStream_t)stream, p); break;
+    case 8: hipLaunchKernelGGL(tree_traverse_kernel<8>, grid, dim3(64), lds, (hipStream_t)stream, p); break;
+    default: hipLaunchKernelGGL(tree_traverse_kernel<0>, grid, dim3(64), lds, (hipStream_t)stream, p); break;
+  }
   return check_launch("tree_traverse_kernel");
 }
 
