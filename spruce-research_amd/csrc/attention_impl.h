@@ -442,6 +442,13 @@ __device__ void capture_group_average(const uint16_t* qst, int RS, int G, int nh
 // unchanged because O and l share the same reference point.
 constexpr float kRescaleThreshold = 8.0f;
 
+// Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x8;
+constexpr int kSchedDsRead = 0x100;
+// LDS fragment reads in flight ahead of the MFMA that consumes them, in
+// K k-steps (two reads each; the V^T loop keeps the same number of reads).
+constexpr int kLookahead = 2;
+
 template <int D, int WAVES, typename TIn, bool F16, int MODE, bool SUMM = false, bool CAP = false, bool PROD = false>
 __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnParams p) {
   static_assert(!CAP || (MODE == kModeCausal && !SUMM && TIn::bytes == 2),
@@ -660,18 +667,25 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
   // l rescale); O^T += V^T P^T.
   f32x16_t sc0, sc1;
   uint4 pk[2][2];
+  // LDS fragment reads are interleaved with the MFMAs that consume them
+  // (kLookahead k-steps ahead, pinned by scheduling-group barriers), so the
+  // waves' LDS traffic overlaps their matrix-core work instead of running as
+  // a separate phase in which all waves of the workgroup contend for LDS.
   auto scores = [&](const uint16_t* Ks) {
     const uint16_t* kp = Ks + l32 * KSTR + 8 * hl;
-    // All K fragments of the block are read before the first MFMA (pinned by
-    // the scheduling barrier), so the matrix cores never wait on a just-issued
-    // LDS read.
     uint4 a0[KS], a1[KS];
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
       a0[kk] = *reinterpret_cast<const uint4*>(kp + 16 * kk);
       a1[kk] = *reinterpret_cast<const uint4*>(kp + 32 * KSTR + 16 * kk);
     }
-    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * kLookahead, 0);
+#pragma unroll
+    for (int i = 0; i < KS - kLookahead; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2 * kLookahead, 0);
     f32x16_t s0 = f32x16_t{}, s1 = f32x16_t{};
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
@@ -745,7 +759,7 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     }
     l_run += psum;
   };
-  // O^T += V^T P^T.  All V^T fragments are read first, as for K;
+  // O^T += V^T P^T, V^T fragments interleaved like the K fragments;
   // consecutive MFMAs go to different output tiles (dt fastest), so no MFMA
   // waits on the previous one's result.
   auto pv = [&](const uint16_t* Vt) {
@@ -756,7 +770,13 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
       const int dt = i % DT, ch = i / DT, c = ch >> 1, h2 = ch & 1;
       va[i] = *reinterpret_cast<const uint4*>(vp + dt * 32 * VSTR + 32 * c + 16 * h2);
     }
-    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * kLookahead, 0);
+#pragma unroll
+    for (int i = 0; i < DT * 4 - 2 * kLookahead; ++i) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2 * kLookahead, 0);
 #pragma unroll
     for (int i = 0; i < DT * 4; ++i) {
       const int dt = i % DT, ch = i / DT, c = ch >> 1, h2 = ch & 1;
