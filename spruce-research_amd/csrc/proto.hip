@@ -64,6 +64,24 @@ __device__ __forceinline__ void store1(void* base, int64_t elem, int dtype, floa
 __device__ __forceinline__ void group_avg8(const ProtoParams& p, int b, int h0, int t, int c, float* dst) {
   const int64_t e0 = (int64_t)b * p.xs[0] + (int64_t)t * p.xs[2] + 8 * c;
   float s[8];
+  if (p.rep > 1 && p.rep <= 8) {
+    // Up to 8 heads: every load is issued before the first add, so the row
+    // costs one memory round trip; the sum is the same ordered sequence.
+    float v[8][8];
+#pragma unroll
+    for (int h = 0; h < 8; ++h)
+      if (h < p.rep) load8f(p.x, e0 + (int64_t)(h0 + h) * p.xs[1], p.dtype, v[h]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s[j] = 0.0f + v[0][j];
+#pragma unroll
+    for (int h = 1; h < 8; ++h)
+      if (h < p.rep)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s[j] = s[j] + v[h][j];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dst[j] = round_to(s[j] * p.inv_rep, p.dtype);
+    return;
+  }
   load8f(p.x, e0 + (int64_t)h0 * p.xs[1], p.dtype, s);
   if (p.rep > 1) {
 #pragma unroll

@@ -70,6 +70,7 @@ struct MergeParams {
   void* parent;       // [S, m, P, D]
   int64_t S;
   int n, m, P, D, radix, dtype;
+  int vec;            // D % 8 == 0 and child 16-byte aligned: 8-element loads
 };
 
 // One wavefront per (slab, parent node).
@@ -88,7 +89,28 @@ __global__ __launch_bounds__(64) void tree_merge_kernel(const MergeParams p) {
   float* mean = feat + ncand * D;     // [D]
   float* dist = mean + D;             // [64]
   const int64_t cbase = ((s * p.n + c0) * p.P) * (int64_t)D;
-  for (int i = lane; i < ncand * D; i += 64) feat[i] = load_elem(p.child, cbase + i, p.dtype);
+  if (p.vec) {
+    // 8 elements per load, up to 4 loads per lane in flight before the LDS
+    // stores (one round trip per 2048 elements).
+    const int nv = ncand * D / 8;
+    for (int v0 = 0; v0 < nv; v0 += 256) {
+      float t[4][8];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int vi = v0 + 64 * u + lane;
+        if (vi < nv) load8f(p.child, cbase + 8 * (int64_t)vi, p.dtype, t[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int vi = v0 + 64 * u + lane;
+        if (vi < nv)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) feat[8 * vi + j] = t[u][j];
+      }
+    }
+  } else {
+    for (int i = lane; i < ncand * D; i += 64) feat[i] = load_elem(p.child, cbase + i, p.dtype);
+  }
   __syncthreads();
   for (int d = lane; d < D; d += 64) {
     float acc = 0.f;
@@ -406,6 +428,7 @@ extern "C" int spruce_tree_merge_level(const void* child, int64_t S, int64_t n, 
   p.D = (int)D;
   p.radix = (int)radix;
   p.dtype = dtype;
+  p.vec = (D % 8 == 0 && ((uintptr_t)child % 16) == 0) ? 1 : 0;
   SPRUCE_REQUIRE(S * p.m < ((int64_t)1 << 31), "too many parent nodes");
   const size_t lds = ((size_t)radix * P * D + D + 64) * sizeof(float);
   SPRUCE_REQUIRE(lds <= 65536, "radix * P * D too large for one workgroup's LDS (%zu bytes)", lds);
