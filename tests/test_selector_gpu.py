@@ -55,6 +55,18 @@ def test_projection_scores_and_topk_are_bit_exact():
     assert np.array_equal(_np(sel), osel.topk(osel.scores(eqp, ekp), 5))
 
 
+@pytest.mark.parametrize("N,D,P", [(1, 4, 4), (65, 96, 36), (200, 256, 128), (130, 160, 68), (33, 6, 5),
+                                   (4096 * 8, 128, 128)])
+def test_projection_shapes_are_bit_exact(N, D, P):
+    # Vector tiles (D % 4 == 0, P % 4 == 0: ragged rows and columns, two
+    # 128-wide slices of D) and the scalar form (D = 6, P = 5).
+    gen = torch.Generator().manual_seed(N + D + P)
+    x = torch.randn(N, D, generator=gen)
+    W = torch.randn(D, P, generator=gen) * 0.1
+    got = project(x.to(DEV), W)
+    assert np.array_equal(_np(got), osel.project(x.numpy(), W.numpy()))
+
+
 def test_scores_with_eight_prototypes_per_side_are_bit_exact():
     # The reference's captured features carry 8 prototypes per block on each
     # side; their tiles exceed LDS, so the direct kernel computes them.
