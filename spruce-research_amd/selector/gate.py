@@ -34,15 +34,21 @@ class FlatGate(nn.Module):
         if torch.is_grad_enabled() and (self.Wq.requires_grad or self.Wk.requires_grad):
             raise RuntimeError("the HIP FlatGate scores only; run it under torch.no_grad()")
 
+    @staticmethod
+    def _project(feat, W):
+        if feat.shape[0] == 1:
+            return project(feat[0].float(), W[0].float()).unsqueeze(0)
+        return torch.stack([project(feat[l].float(), W[l].float()) for l in range(feat.shape[0])])
+
     @torch.no_grad()
     def project_queries(self, q_feat):
         """[L,G,qb,P,d] -> [L,G,qb,P,p] (selector/gate.py:120-122)."""
-        return torch.stack([project(q_feat[l].float(), self.Wq[l].float()) for l in range(q_feat.shape[0])])
+        return self._project(q_feat, self.Wq)
 
     @torch.no_grad()
     def project_keys(self, k_feat):
         """[L,G,kb,P,d] -> [L,G,kb,P,p] (selector/gate.py:124-127)."""
-        return torch.stack([project(k_feat[l].float(), self.Wk[l].float()) for l in range(k_feat.shape[0])])
+        return self._project(k_feat, self.Wk)
 
     @torch.no_grad()
     def score_projected_candidates(self, projected_q, projected_k, candidate_ids, layer_chunk=1):

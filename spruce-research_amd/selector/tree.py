@@ -63,6 +63,23 @@ def level_ranges(num_leaves, level, radix, device=None):
     return starts, (starts + span).clamp_max(num_leaves)
 
 
+def _level_range_table(num_leaves, radix, device):
+    """level_ranges of every level (leaf first), computed on the host and
+    moved to the device in one copy; returns per-level (starts, ends) views."""
+    counts, spans = [num_leaves], [1]
+    while counts[-1] > 1:
+        counts.append((counts[-1] + radix - 1) // radix)
+        spans.append(spans[-1] * radix)
+    starts = torch.cat([torch.arange(c, dtype=torch.long) * sp for c, sp in zip(counts, spans)])
+    widths = torch.repeat_interleave(torch.tensor(spans, dtype=torch.long), torch.tensor(counts))
+    table = torch.stack([starts, (starts + widths).clamp_max(num_leaves)]).to(device)
+    out, off = [], 0
+    for c in counts:
+        out.append((table[0, off:off + c], table[1, off:off + c]))
+        off += c
+    return out
+
+
 def merge_level(features, radix=2):
     """One parent level: [L,G,n,P,d] -> [L,G,ceil(n/radix),P,d] (HIP)."""
     _validate_radix(radix)
@@ -87,17 +104,15 @@ def build_key_tree(k_feat, radix=2):
     _validate_radix(radix)
     if k_feat.dim() != 5:
         raise ValueError(f"k_feat must be [L,G,kb,P,d], got {tuple(k_feat.shape)}")
-    device = k_feat.device
     kb = k_feat.shape[2]
-    starts, ends = level_ranges(kb, 0, radix, device)
-    levels = [KeyTreeLevel(0, k_feat, starts, ends)]
+    ranges = _level_range_table(kb, radix, k_feat.device)
+    levels = [KeyTreeLevel(0, k_feat, *ranges[0])]
     current = k_feat
     level = 0
     while current.shape[2] > 1:
         level += 1
         current = merge_level(current, radix)
-        starts, ends = level_ranges(kb, level, radix, device)
-        levels.append(KeyTreeLevel(level, current, starts, ends))
+        levels.append(KeyTreeLevel(level, current, *ranges[level]))
     return levels
 
 

@@ -46,6 +46,17 @@ def test_reference_layout_known_answers():
         tree_node_counts(5, radix=1)
 
 
+def test_level_range_table_equals_per_level_ranges():
+    # build_key_tree takes every level's ranges from one host-built table.
+    from selector.tree import _level_range_table
+    for kb, radix in ((5, 2), (2048, 2), (1, 2), (10, 3), (7, 2), (81, 3)):
+        table = _level_range_table(kb, radix, "cpu")
+        assert len(table) == len(otree.level_counts(kb, radix))
+        for v, (starts, ends) in enumerate(table):
+            want_s, want_e = level_ranges(kb, v, radix)
+            assert torch.equal(starts, want_s) and torch.equal(ends, want_e), (kb, radix, v)
+
+
 @pytest.mark.parametrize("radix,P,n,D", [(2, 4, 7, 5), (3, 4, 7, 5), (2, 8, 9, 16), (2, 1, 5, 8), (3, 3, 10, 12)])
 def test_merge_matches_float64_reference_form(radix, P, n, D):
     rng = np.random.default_rng(radix * 100 + P * 10 + n)
