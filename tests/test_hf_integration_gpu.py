@@ -8,6 +8,9 @@ random weights (2 layers, 7 query heads over 1 KV head, head_dim 64).
   HIP sparse-prefill attention with every causal block selected gives the
   same last hidden state as torch's dense causal SDPA.  Bar: 2e-2 max-abs and
   1e-3 mean-abs after normalising by the hidden state's RMS.
+* Prefill then decode: the cached one-token step goes to SDPA (decode stays
+  dense, kernels/sparse_prefill.py:63-66 there); last-token and decoded
+  logits within 2e-2 of the logits RMS of a bf16-input SDPA run, same token.
 * Teacher capture (get_pooled_targets, teacher/chunked_extract.py:216-265
   there): per-layer pooled mass equals pool_attention of the model's eager
   attention maps (the reference's integration check,
@@ -97,3 +100,39 @@ def test_get_pooled_targets_matches_eager_attention_maps():
         d = (pooled[:, layer] - ref).abs() / 64
         print(f"layer {layer} mass: max_abs={d.max().item():.3e} mean_abs={d.mean().item():.3e}", flush=True)
         assert d.max().item() <= 2e-2 and d.mean().item() <= 1e-3
+
+
+@torch.no_grad()
+def test_prefill_then_decode_dispatches_decode_to_sdpa():
+    # SPRUCE keeps decode dense (kernels/sparse_prefill.py:63-66 in the
+    # reference): the cached one-token step goes to SDPA with its mask while
+    # selected_blocks keeps being forwarded.  Logits of the prefill's last
+    # token and of the decoded token match a bf16-input SDPA run.
+    model = _model()
+    T = 200
+    ids = torch.randint(0, 256, (1, T), generator=torch.Generator().manual_seed(3)).to(DEV)
+    qb = (T + 63) // 64
+    sel = torch.full((1, 2, 1, qb, qb), -1, dtype=torch.int32)
+    for q in range(qb):
+        sel[0, :, 0, q, : q + 1] = torch.arange(q + 1, dtype=torch.int32)
+    sel = sel.to(DEV)
+
+    def run(name):
+        _set_impl(model, name)
+        out = model(input_ids=ids, use_cache=True, selected_blocks=sel, block_size=64)
+        nxt = out.logits[:, -1:].argmax(-1)
+        step = model(input_ids=nxt, past_key_values=out.past_key_values, use_cache=True,
+                     selected_blocks=sel, block_size=64)
+        return out.logits[:, -1], step.logits[:, -1], nxt
+
+    from transformers import AttentionInterface
+    from kernels.sparse_prefill import register_triton_sparse_prefill_attention
+    AttentionInterface.register("bf16_input_sdpa", _bf16_input_sdpa)
+    dense_last, dense_step, dense_next = run("bf16_input_sdpa")
+    sparse_last, sparse_step, sparse_next = run(register_triton_sparse_prefill_attention())
+    for a, b in ((sparse_last, dense_last), (sparse_step, dense_step)):
+        rms = b.pow(2).mean().sqrt()
+        d = ((a - b).abs() / rms).max().item()
+        print(f"logits max_abs/rms={d:.3e}", flush=True)
+        assert d <= 2e-2
+    assert torch.equal(sparse_next, dense_next)
