@@ -24,7 +24,11 @@
 //     and 3 swapped), so every MFMA operand is one 16-byte LDS read;
 //   * K/V staging is double-buffered: the next block's global loads are in
 //     flight while the current block is on the matrix cores; one barrier per
-//     block;
+//     block.  When a workgroup has a wave without a tile (G = 3, 5, 6, 7 in
+//     8-wave workgroups) that wave stages every block alone (the producer
+//     form) and the tile waves only compute;
+//   * LDS fragment reads are interleaved with the MFMAs that consume them, so
+//     the waves' LDS traffic overlaps the matrix cores;
 //   * skipped blocks are never touched: the block list is walked once and only
 //     listed blocks are loaded.
 //
