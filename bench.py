@@ -353,7 +353,7 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
             "traffic": _traffic("cfg2_32k_block_mask"),
-            "kernel": "sparse_prefill_kernel<128, 7, InBF16, false, kModeMask>",
+            "kernel": "sparse_prefill_kernel<128, 8, InBF16, false, 2, false, false, true> (block mask, producer wave)",
             "kernel_ms_mean": round(kmean, 4),
         },
         "cpu_baseline": cpu,
