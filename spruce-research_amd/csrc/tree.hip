@@ -85,9 +85,10 @@ __global__ __launch_bounds__(64) void tree_merge_kernel(const MergeParams p) {
   const int cn = p.n - c0 < p.radix ? p.n - c0 : p.radix;  // valid children
   const int ncand = cn * p.P;
   const int D = p.D;
-  float* feat = sh;                   // [ncand, D]
-  float* mean = feat + ncand * D;     // [D]
-  float* dist = mean + D;             // [64]
+  // Rows padded to D + 4 floats: 16-byte aligned and spread over the banks.
+  const int FS = D + 4;
+  float* feat = sh;                   // [ncand, FS]
+  float* mean = feat + ncand * FS;    // [D]
   const int64_t cbase = ((s * p.n + c0) * p.P) * (int64_t)D;
   if (p.vec) {
     // 8 elements per load, up to 4 loads per lane in flight before the LDS
@@ -103,46 +104,67 @@ __global__ __launch_bounds__(64) void tree_merge_kernel(const MergeParams p) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int vi = v0 + 64 * u + lane;
-        if (vi < nv)
+        if (vi < nv) {
+          const int row = (8 * vi) / D, col = 8 * vi - row * D;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) feat[8 * vi + j] = t[u][j];
+          for (int j = 0; j < 8; ++j) feat[row * FS + col + j] = t[u][j];
+        }
       }
     }
   } else {
-    for (int i = lane; i < ncand * D; i += 64) feat[i] = load_elem(p.child, cbase + i, p.dtype);
+    for (int i = lane; i < ncand * D; i += 64) feat[(i / D) * FS + i % D] = load_elem(p.child, cbase + i, p.dtype);
   }
   __syncthreads();
   for (int d = lane; d < D; d += 64) {
     float acc = 0.f;
-    for (int c = 0; c < cn; ++c) acc = acc + feat[(c * p.P) * D + d];
+    for (int c = 0; c < cn; ++c) acc = acc + feat[(c * p.P) * FS + d];
     mean[d] = model_round(model_round(acc, p.dtype) / (float)cn, p.dtype);
   }
   __syncthreads();
+  // Distances in registers: lane i holds candidate i's (dims in order).
+  float dist = 0.f;
   if (lane < ncand) {
     float acc = 0.f;
-    const float* x = feat + lane * D;
-    for (int d = 0; d < D; ++d) {
-      const float df = x[d] - mean[d];
-      acc = acc + df * df;
+    const float* x = feat + lane * FS;
+    if ((D & 3) == 0) {
+#pragma unroll 8
+      for (int d = 0; d < D; d += 4) {
+        const float4 xv = *reinterpret_cast<const float4*>(x + d);
+        const float4 mv = *reinterpret_cast<const float4*>(mean + d);
+        float df = xv.x - mv.x;
+        acc = acc + df * df;
+        df = xv.y - mv.y;
+        acc = acc + df * df;
+        df = xv.z - mv.z;
+        acc = acc + df * df;
+        df = xv.w - mv.w;
+        acc = acc + df * df;
+      }
+    } else {
+      for (int d = 0; d < D; ++d) {
+        const float df = x[d] - mean[d];
+        acc = acc + df * df;
+      }
     }
-    dist[lane] = acc;
+    dist = acc;
   }
-  __syncthreads();
   const int64_t pbase = (s * p.m + j) * (int64_t)p.P * D;
   for (int d = lane; d < D; d += 64) store_elem(p.parent, pbase + d, mean[d], p.dtype);
   if (p.P > 1) {
     int rank = 64;
     if (lane < ncand) {
       rank = 0;
-      const float mine = dist[lane];
-      for (int o = 0; o < ncand; ++o) rank += ranks_before(dist[o], o, mine, lane) ? 1 : 0;
+      for (int o = 0; o < ncand; ++o) {
+        const float od = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, dist), o));
+        rank += ranks_before(od, o, dist, lane) ? 1 : 0;
+      }
     }
-    // Each selected candidate's lane writes its vector to slot 1 + rank.
-    for (int src = 0; src < ncand; ++src) {
-      const int r = __shfl(rank, src);
-      if (r < p.P - 1)
-        for (int d = lane; d < D; d += 64)
-          store_elem(p.parent, pbase + (int64_t)(1 + r) * D + d, feat[src * D + d], p.dtype);
+    // Slot 1 + r takes the candidate of rank r (ranks are a permutation of
+    // 0..ncand-1, and ncand >= P > P - 1).
+    for (int r = 0; r < p.P - 1; ++r) {
+      const int src = __builtin_ctzll(__ballot(rank == r));
+      for (int d = lane; d < D; d += 64)
+        store_elem(p.parent, pbase + (int64_t)(1 + r) * D + d, feat[src * FS + d], p.dtype);
     }
   }
 }
@@ -430,7 +452,7 @@ extern "C" int spruce_tree_merge_level(const void* child, int64_t S, int64_t n, 
   p.dtype = dtype;
   p.vec = (D % 8 == 0 && ((uintptr_t)child % 16) == 0) ? 1 : 0;
   SPRUCE_REQUIRE(S * p.m < ((int64_t)1 << 31), "too many parent nodes");
-  const size_t lds = ((size_t)radix * P * D + D + 64) * sizeof(float);
+  const size_t lds = ((size_t)radix * P * (D + 4) + D) * sizeof(float);
   SPRUCE_REQUIRE(lds <= 65536, "radix * P * D too large for one workgroup's LDS (%zu bytes)", lds);
   hipLaunchKernelGGL(tree_merge_kernel, dim3((unsigned)(S * p.m)), dim3(64), lds, (hipStream_t)stream, p);
   return check_launch("tree_merge_kernel");
