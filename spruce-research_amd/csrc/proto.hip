@@ -109,8 +109,10 @@ __device__ __forceinline__ float group_avg1(const ProtoParams& p, int b, int h0,
 }
 
 __global__ __launch_bounds__(256) void proto_pool_kernel(ProtoParams p) {
-  __shared__ float tile[kProtoMaxBlock][kProtoMaxD + 1];
-  __shared__ float mean[kProtoMaxD];
+  // Rows padded to D + 4 floats: 16-byte aligned for the float4 distance
+  // reads and spread over the banks.
+  __shared__ __attribute__((aligned(16))) float tile[kProtoMaxBlock][kProtoMaxD + 4];
+  __shared__ __attribute__((aligned(16))) float mean[kProtoMaxD];
   __shared__ int pick[kProtoMaxP];
   const int tid = threadIdx.x;
   const int i = blockIdx.x % p.nb;
@@ -141,6 +143,7 @@ __global__ __launch_bounds__(256) void proto_pool_kernel(ProtoParams p) {
 
   if (tid < p.D) {
     float s = 0.0f;
+#pragma unroll 8
     for (int t = 0; t < n; ++t) s = s + tile[t][tid];
     mean[tid] = round_to(round_to(s, p.dtype) / (float)n, p.dtype);
   }
@@ -152,9 +155,25 @@ __global__ __launch_bounds__(256) void proto_pool_kernel(ProtoParams p) {
     float dist = -__builtin_inff();
     if (tid < n) {
       float s = 0.0f;
-      for (int d = 0; d < p.D; ++d) {
-        const float diff = tile[tid][d] - mean[d];
-        s = s + diff * diff;
+      if ((p.D & 3) == 0) {
+#pragma unroll 8
+        for (int d = 0; d < p.D; d += 4) {
+          const float4 x = *reinterpret_cast<const float4*>(&tile[tid][d]);
+          const float4 m = *reinterpret_cast<const float4*>(&mean[d]);
+          float diff = x.x - m.x;
+          s = s + diff * diff;
+          diff = x.y - m.y;
+          s = s + diff * diff;
+          diff = x.z - m.z;
+          s = s + diff * diff;
+          diff = x.w - m.w;
+          s = s + diff * diff;
+        }
+      } else {
+        for (int d = 0; d < p.D; ++d) {
+          const float diff = tile[tid][d] - mean[d];
+          s = s + diff * diff;
+        }
       }
       dist = s;
     }
