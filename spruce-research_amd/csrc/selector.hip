@@ -393,6 +393,116 @@ __global__ __launch_bounds__(256) void gate_scores_kernel(const ScoreParams p) {
   }
 }
 
+// The same scores, register-blocked, for one query prototype and PK (1 or 2)
+// key prototypes: a workgroup covers 64 query blocks x 64 key blocks and
+// thread (tr, tc) holds query blocks 4tr..4tr+3 x key blocks 4tc..4tc+3 for
+// every key prototype. The prototypes are staged transposed ([e][block]) in
+// slices of kGS dims, so each step over e reads one float4 of query values
+// and PK float4 of key values for 16 * PK fmaf (the kernel above reads five
+// float4 for 16). Same operation order as the kernel above.
+constexpr int kGT = 64, kGS = 32, kGRow = kGT + 4;  // tile, slice, padded LDS row (floats)
+template <int PK>
+__global__ __launch_bounds__(256) void gate_scores_tile_kernel(const ScoreParams p) {
+  __shared__ __attribute__((aligned(16))) float xs[kGS * kGRow];
+  __shared__ __attribute__((aligned(16))) float ys[PK * kGS * kGRow];
+  const int bg = blockIdx.z;
+  const int i0 = blockIdx.x * kGT, j0 = blockIdx.y * kGT;
+  const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
+  float* out = p.scores + (int64_t)bg * p.Qb * p.Kb;
+  if (p.causal && j0 > i0 + kGT - 1) {
+    // Entirely above the diagonal.
+    for (int r = 0; r < 4; ++r) {
+      const int i = i0 + 4 * tr + r;
+      for (int k = 0; k < 4; ++k) {
+        const int j = j0 + 4 * tc + k;
+        if (i < p.Qb && j < p.Kb) out[(int64_t)i * p.Kb + j] = -INFINITY;
+      }
+    }
+    return;
+  }
+  const float* qsrc = p.qp + (int64_t)bg * p.Qb * p.P;
+  const float* ksrc = p.kp + (int64_t)bg * p.Kb * PK * p.P;
+  float acc[PK][4][4];
+#pragma unroll
+  for (int c = 0; c < PK; ++c)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc[c][r][k] = 0.f;
+  // Staging map: kD4 consecutive lanes read one block's slice (contiguous).
+  constexpr int kD4 = kGS / 4;                  // float4 per block slice
+  constexpr int kLoads = kGT * kD4 / 256;       // float4 per thread per operand
+  for (int e0 = 0; e0 < p.P; e0 += kGS) {
+    float4 qv[kLoads], kv[PK][kLoads];
+#pragma unroll
+    for (int t = 0; t < kLoads; ++t) {
+      const int idx = tid + 256 * t, blk = idx / kD4, d4 = idx % kD4;
+      const int i = i0 + blk, j = j0 + blk;
+      qv[t] = i < p.Qb ? *reinterpret_cast<const float4*>(qsrc + (int64_t)i * p.P + e0 + 4 * d4)
+                       : float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < PK; ++c)
+        kv[c][t] = j < p.Kb ? *reinterpret_cast<const float4*>(ksrc + ((int64_t)j * PK + c) * p.P + e0 + 4 * d4)
+                            : float4{0.f, 0.f, 0.f, 0.f};
+    }
+    __syncthreads();  // the previous slice has been read
+#pragma unroll
+    for (int t = 0; t < kLoads; ++t) {
+      const int idx = tid + 256 * t, blk = idx / kD4, d4 = idx % kD4;
+      float* x = xs + 4 * d4 * kGRow + blk;
+      x[0] = qv[t].x;
+      x[kGRow] = qv[t].y;
+      x[2 * kGRow] = qv[t].z;
+      x[3 * kGRow] = qv[t].w;
+#pragma unroll
+      for (int c = 0; c < PK; ++c) {
+        float* y = ys + (c * kGS + 4 * d4) * kGRow + blk;
+        y[0] = kv[c][t].x;
+        y[kGRow] = kv[c][t].y;
+        y[2 * kGRow] = kv[c][t].z;
+        y[3 * kGRow] = kv[c][t].w;
+      }
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (int e = 0; e < kGS; ++e) {
+      const float4 x4 = *reinterpret_cast<const float4*>(xs + e * kGRow + 4 * tr);
+      const float x[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+      for (int c = 0; c < PK; ++c) {
+        const float4 y4 = *reinterpret_cast<const float4*>(ys + (c * kGS + e) * kGRow + 4 * tc);
+        const float y[4] = {y4.x, y4.y, y4.z, y4.w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) acc[c][r][k] = __builtin_fmaf(x[r], y[k], acc[c][r][k]);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int i = i0 + 4 * tr + r;
+    if (i >= p.Qb) continue;
+    float v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int j = j0 + 4 * tc + k;
+      float best = acc[0][r][k];
+#pragma unroll
+      for (int c = 1; c < PK; ++c) best = acc[c][r][k] > best ? acc[c][r][k] : best;
+      v[k] = (!p.causal || j <= i) ? best / p.div : -INFINITY;
+    }
+    float* o = out + (int64_t)i * p.Kb + j0 + 4 * tc;
+    if (j0 + 4 * tc + 3 < p.Kb && (p.Kb & 3) == 0) {
+      *reinterpret_cast<float4*>(o) = float4{v[0], v[1], v[2], v[3]};
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (j0 + 4 * tc + k < p.Kb) o[k] = v[k];
+    }
+  }
+}
+
 // The same scores for prototype counts whose tiles do not fit in LDS (e.g.
 // 8 x 8 prototypes of 128 dims): one thread per score, operands read through
 // the cache, identical operation order.
@@ -634,6 +744,14 @@ extern "C" int spruce_gate_scores(const float* qp, const float* kp, int64_t BG, 
     hipLaunchKernelGGL(gate_scores_direct_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, p,
                        total);
     return check_launch("gate_scores_direct_kernel");
+  }
+  if (Pq == 1 && (Pk == 1 || Pk == 2) && P % kGS == 0 && reinterpret_cast<uintptr_t>(scores) % 16 == 0) {
+    const dim3 grid((unsigned)((Qb + kGT - 1) / kGT), (unsigned)((Kb + kGT - 1) / kGT), (unsigned)BG);
+    if (Pk == 1)
+      hipLaunchKernelGGL(gate_scores_tile_kernel<1>, grid, dim3(256), 0, (hipStream_t)stream, p);
+    else
+      hipLaunchKernelGGL(gate_scores_tile_kernel<2>, grid, dim3(256), 0, (hipStream_t)stream, p);
+    return check_launch("gate_scores_tile_kernel");
   }
   const dim3 grid((unsigned)((Qb + kTI - 1) / kTI), (unsigned)((Kb + kTJ - 1) / kTJ), (unsigned)BG);
   if (lds > 64 * 1024) {

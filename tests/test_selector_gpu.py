@@ -67,6 +67,22 @@ def test_projection_shapes_are_bit_exact(N, D, P):
     assert np.array_equal(_np(got), osel.project(x.numpy(), W.numpy()))
 
 
+@pytest.mark.parametrize("S,Qb,Kb,Pk,P", [
+    (2, 130, 130, 2, 128),   # register-blocked tiles: ragged last tile row and column
+    (1, 77, 190, 1, 64),     # one key prototype, Qb != Kb
+    (3, 64, 67, 2, 32),      # Kb % 4 != 0: scalar stores at the row ends
+    (1, 200, 200, 2, 48),    # P % 32 != 0: the LDS-broadcast tile kernel
+    (1, 1, 1, 2, 128),
+])
+def test_score_tile_shapes_are_bit_exact(S, Qb, Kb, Pk, P):
+    gen = torch.Generator().manual_seed(Qb * 7 + Kb + P)
+    qp = torch.randn(S, Qb, 1, P, generator=gen)
+    kp = torch.randn(S, Kb, Pk, P, generator=gen)
+    for causal in (True, False):
+        got = gate_scores(qp.to(DEV), kp.to(DEV), causal=causal)
+        assert np.array_equal(_np(got), osel.scores(qp.numpy(), kp.numpy(), causal=causal)), causal
+
+
 def test_scores_with_eight_prototypes_per_side_are_bit_exact():
     # The reference's captured features carry 8 prototypes per block on each
     # side; their tiles exceed LDS, so the direct kernel computes them.
