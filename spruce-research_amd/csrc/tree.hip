@@ -208,41 +208,39 @@ __device__ __forceinline__ float maxsim_one(const float* qrow, const float* krow
   return best;
 }
 
-// Two (candidate, key prototype) pairs per lane against a compile-time
-// number of query prototypes: every query float4 read from LDS feeds both
-// pairs, and each chain is the same fmaf sequence as maxsim_one (e
-// ascending), so the results are identical.  The key vectors stream in
-// 64-byte pieces (4 float4 loads back to back, the next piece in flight
-// while the current one is used): lanes read different vectors, and taking
-// a line in two pieces close together keeps it in L1 between them, where
-// one float4 per step was refetched from L2 for every 16 bytes (measured
-// 1.85 -> 1.0-1.1 ms at the cfg5 grid).  Requires pd % 16 == 0.
-template <int PQ>
-__device__ __forceinline__ void maxsim_pair(const float* qrow, const float* ka, const float* kb, int pd, float& ra,
-                                            float& rb) {
-  constexpr int CW = 4;  // float4 per piece
-  float acc0[PQ], acc1[PQ];
+// NP (candidate, key prototype) pairs per lane against a compile-time number
+// of query prototypes: every query float4 read from LDS feeds all NP pairs,
+// and each chain is the same fmaf sequence as maxsim_one (e ascending), so
+// the results are identical.  The key vectors stream in pieces of CW float4
+// (loads back to back, the next piece in flight while the current one is
+// used): lanes read different vectors, and taking a line in a few pieces
+// close together keeps it in L1 between them, where one float4 per step was
+// refetched from L2 for every 16 bytes (measured 1.85 -> 1.0-1.1 ms at the
+// cfg5 grid).  Requires pd % (4 * CW) == 0.
+template <int PQ, int NP, int CW>
+__device__ __forceinline__ void maxsim_multi(const float* qrow, const float* const (&kv)[NP], int pd,
+                                             float (&res)[NP]) {
+  float acc[NP][PQ];
 #pragma unroll
-  for (int a = 0; a < PQ; ++a) acc0[a] = acc1[a] = 0.f;
-  float4 na[CW], nb[CW];
+  for (int n = 0; n < NP; ++n)
 #pragma unroll
-  for (int j = 0; j < CW; ++j) {
-    na[j] = *reinterpret_cast<const float4*>(ka + 4 * j);
-    nb[j] = *reinterpret_cast<const float4*>(kb + 4 * j);
-  }
+    for (int a = 0; a < PQ; ++a) acc[n][a] = 0.f;
+  float4 nxt[NP][CW];
+#pragma unroll
+  for (int n = 0; n < NP; ++n)
+#pragma unroll
+    for (int j = 0; j < CW; ++j) nxt[n][j] = *reinterpret_cast<const float4*>(kv[n] + 4 * j);
   for (int e0 = 0; e0 < pd; e0 += 4 * CW) {
-    float4 ca[CW], cb[CW];
+    float4 cur[NP][CW];
 #pragma unroll
-    for (int j = 0; j < CW; ++j) {
-      ca[j] = na[j];
-      cb[j] = nb[j];
-    }
+    for (int n = 0; n < NP; ++n)
+#pragma unroll
+      for (int j = 0; j < CW; ++j) cur[n][j] = nxt[n][j];
     if (e0 + 4 * CW < pd) {
 #pragma unroll
-      for (int j = 0; j < CW; ++j) {
-        na[j] = *reinterpret_cast<const float4*>(ka + e0 + 4 * CW + 4 * j);
-        nb[j] = *reinterpret_cast<const float4*>(kb + e0 + 4 * CW + 4 * j);
-      }
+      for (int n = 0; n < NP; ++n)
+#pragma unroll
+        for (int j = 0; j < CW; ++j) nxt[n][j] = *reinterpret_cast<const float4*>(kv[n] + e0 + 4 * CW + 4 * j);
     }
 #pragma unroll
     for (int j = 0; j < CW; ++j) {
@@ -250,29 +248,32 @@ __device__ __forceinline__ void maxsim_pair(const float* qrow, const float* ka, 
 #pragma unroll
       for (int a = 0; a < PQ; ++a) {
         const float4 q4 = *reinterpret_cast<const float4*>(qrow + a * pd + e);
-        float t = acc0[a], u = acc1[a];
-        t = fmaf(q4.x, ca[j].x, t);
-        u = fmaf(q4.x, cb[j].x, u);
-        t = fmaf(q4.y, ca[j].y, t);
-        u = fmaf(q4.y, cb[j].y, u);
-        t = fmaf(q4.z, ca[j].z, t);
-        u = fmaf(q4.z, cb[j].z, u);
-        t = fmaf(q4.w, ca[j].w, t);
-        u = fmaf(q4.w, cb[j].w, u);
-        acc0[a] = t;
-        acc1[a] = u;
+#pragma unroll
+        for (int n = 0; n < NP; ++n) {
+          float t = acc[n][a];
+          t = fmaf(q4.x, cur[n][j].x, t);
+          t = fmaf(q4.y, cur[n][j].y, t);
+          t = fmaf(q4.z, cur[n][j].z, t);
+          t = fmaf(q4.w, cur[n][j].w, t);
+          acc[n][a] = t;
+        }
       }
     }
   }
-  float x = acc0[0], y = acc1[0];
 #pragma unroll
-  for (int a = 1; a < PQ; ++a) {
-    if (acc0[a] > x) x = acc0[a];
-    if (acc1[a] > y) y = acc1[a];
+  for (int n = 0; n < NP; ++n) {
+    float x = acc[n][0];
+#pragma unroll
+    for (int a = 1; a < PQ; ++a)
+      if (acc[n][a] > x) x = acc[n][a];
+    res[n] = x;
   }
-  ra = x;
-  rb = y;
 }
+
+// Two pairs per lane in 64-byte pieces.  Measured at the cfg5 grid against
+// 1.0-1.06 ms: four pairs in 64-byte pieces 1.68 ms (289 registers), four in
+// 32-byte pieces 1.10 ms, four or eight in 16-byte pieces 1.77-2.03 ms.
+constexpr int kTravNP = 2, kTravCW = 4;
 
 struct TraverseParams {
   ScoreParams2 sc;
@@ -317,20 +318,26 @@ __global__ __launch_bounds__(64) void tree_traverse_kernel(const TraverseParams 
     __syncthreads();
     const float* kl = sc.kp + (s * sc.N + p.offset[v]) * (int64_t)sc.Pk * sc.pd;
     const int npairs = ncand * sc.Pk;
-    if (PQ > 0 && sc.pd % 16 == 0) {
-      // Pairs pr and pr + 64; an invalid or missing pair reads the level's
-      // first node (always in range) and its result is dropped.
-      for (int pr = lane; pr < npairs; pr += 128) {
-        const int pr2 = pr + 64;
-        const int i0 = pr / sc.Pk, c0 = pr - i0 * sc.Pk;
-        const int i1 = pr2 < npairs ? pr2 / sc.Pk : 0, c1 = pr2 < npairs ? pr2 - i1 * sc.Pk : 0;
-        const bool v0 = valid[i0] != 0, v1 = pr2 < npairs && valid[i1] != 0;
-        const float* k0 = kl + (v0 ? ((int64_t)cand[i0] * sc.Pk + c0) * sc.pd : 0);
-        const float* k1 = kl + (v1 ? ((int64_t)cand[i1] * sc.Pk + c1) * sc.pd : 0);
-        float m0, m1;
-        maxsim_pair<PQ == 0 ? 1 : PQ>(qrow, k0, k1, sc.pd, m0, m1);
-        pm[i0 * sc.Pk + c0] = v0 ? m0 : 0.f;
-        if (pr2 < npairs) pm[i1 * sc.Pk + c1] = v1 ? m1 : 0.f;
+    if (PQ > 0 && sc.pd % (4 * kTravCW) == 0) {
+      // Pairs pr + 64 n (n < kTravNP); an invalid or missing pair reads the
+      // level's first node (always in range) and its result is dropped.
+      for (int pr = lane; pr < npairs; pr += 64 * kTravNP) {
+        int idx[kTravNP], cc[kTravNP];
+        bool ok[kTravNP];
+        const float* kv[kTravNP];
+#pragma unroll
+        for (int n = 0; n < kTravNP; ++n) {
+          const int pn = pr + 64 * n;
+          idx[n] = pn < npairs ? pn / sc.Pk : 0;
+          cc[n] = pn < npairs ? pn - idx[n] * sc.Pk : 0;
+          ok[n] = pn < npairs && valid[idx[n]] != 0;
+          kv[n] = kl + (ok[n] ? ((int64_t)cand[idx[n]] * sc.Pk + cc[n]) * sc.pd : 0);
+        }
+        float m[kTravNP];
+        maxsim_multi<PQ == 0 ? 1 : PQ, kTravNP, kTravCW>(qrow, kv, sc.pd, m);
+#pragma unroll
+        for (int n = 0; n < kTravNP; ++n)
+          if (pr + 64 * n < npairs) pm[idx[n] * sc.Pk + cc[n]] = ok[n] ? m[n] : 0.f;
       }
     } else {
       for (int pr = lane; pr < npairs; pr += 64) {
