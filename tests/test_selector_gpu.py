@@ -112,6 +112,22 @@ def test_topk_ties_short_rows_and_negative_zero():
     assert _np(got)[0, 10].tolist() == list(range(11)) + [-1] * 21
 
 
+def test_topk_search_boundaries():
+    # Rows with heavy ties, a one-ulp gap at the k-th key, exactly k tied top
+    # keys, a tie across the boundary and full 1024-key rows.
+    gen = torch.Generator().manual_seed(5)
+    s = torch.randn(3, 1024, 1024, generator=gen)
+    s[1] = torch.round(s[1] * 4) / 4
+    row = s[2, 700, :701]
+    order = torch.argsort(row, descending=True, stable=True)
+    kth = row[order[31]].item()
+    s[2, 700, order[32]] = float(np.nextafter(np.float32(kth), np.float32(-np.inf)))
+    s[2, 800, torch.randperm(801, generator=gen)[:32]] = 5.0
+    s[2, 900, torch.randperm(901, generator=gen)[:33]] = 5.0     # the tie crosses the boundary
+    got = causal_topk_blocks(s.to(DEV), 32)
+    assert np.array_equal(_np(got), osel.topk(s.numpy(), 32))
+
+
 def test_flat_gate_matches_reference_bruteforce():
     # Reference tests/test_gate_maxsim.py:22-33 on the HIP scorer.
     torch.manual_seed(0)
