@@ -294,6 +294,105 @@ __global__ __launch_bounds__(256) void project_tile_kernel(const float* __restri
   }
 }
 
+// Large-N form of the kernel above: a TR x TC register tile per thread
+// (16 x 16 threads, a 16TR x 16TC output tile per workgroup) and d staged in
+// slices of kBD, so each step reads TR / 4 + TC / 4 float4 from LDS for
+// TR * TC FMAs (8 x 4: 96 bytes per FMA instruction against 128 for 4 x 4,
+// whose reads alone keep the LDS busy). Same fmaf chain per output (d in
+// order from 0), so the results are identical. Requires D % 4 == 0,
+// P % 4 == 0 and 16-byte aligned operands.
+constexpr int kBD = 32;
+// 8 x 4 per thread from 16K rows (fewer rows leave CUs idle with 128-row
+// tiles). Measured at p = d = 128: N = 131072 0.102 -> 0.068 ms, N = 65536
+// 0.056 -> 0.039 ms; 8 x 8 and 4 x 8 within 5% of 8 x 4.
+constexpr int kBlockProjectRows = 16384, kBlockProjectTR = 8, kBlockProjectTC = 4;
+template <int TR, int TC>
+__global__ __launch_bounds__(256) void project_block_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                            int64_t N, int D, int P, float* __restrict__ out) {
+  constexpr int R = 16 * TR, C = 16 * TC;          // workgroup tile
+  constexpr int XL = R * kBD / 4 / 256;            // x float4 per thread per slice
+  constexpr int WL = C * kBD / 4 / 256;            // w float4 per thread per slice
+  __shared__ __attribute__((aligned(16))) float xs[kBD][R + 4];
+  __shared__ __attribute__((aligned(16))) float ws[kBD][C];
+  const int tid = threadIdx.x;
+  const int tr = tid >> 4, tc = tid & 15;
+  const int64_t n0 = (int64_t)blockIdx.x * R;
+  const int j0 = blockIdx.y * C;
+  float acc[TR][TC];
+#pragma unroll
+  for (int a = 0; a < TR; ++a)
+#pragma unroll
+    for (int c = 0; c < TC; ++c) acc[a][c] = 0.f;
+  for (int d0 = 0; d0 < D; d0 += kBD) {
+    const int dn = D - d0 < kBD ? D - d0 : kBD;
+    float4 xv[XL], wv[WL];
+#pragma unroll
+    for (int t = 0; t < XL; ++t) {
+      const int e = tid + 256 * t, r = e / (kBD / 4), c4 = e % (kBD / 4);
+      const int64_t n = n0 + r;
+      xv[t] = (n < N && 4 * c4 < dn) ? *reinterpret_cast<const float4*>(x + n * D + d0 + 4 * c4)
+                                     : float4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int t = 0; t < WL; ++t) {
+      const int e = tid + 256 * t, dd = e / (C / 4), c4 = e % (C / 4);
+      const int j = j0 + 4 * c4;
+      wv[t] = (dd < dn && j < P) ? *reinterpret_cast<const float4*>(w + (int64_t)(d0 + dd) * P + j)
+                                 : float4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (d0 > 0) __syncthreads();  // the previous slice's reads are done
+#pragma unroll
+    for (int t = 0; t < XL; ++t) {
+      const int e = tid + 256 * t, r = e / (kBD / 4), c4 = e % (kBD / 4);
+      xs[4 * c4][r] = xv[t].x;
+      xs[4 * c4 + 1][r] = xv[t].y;
+      xs[4 * c4 + 2][r] = xv[t].z;
+      xs[4 * c4 + 3][r] = xv[t].w;
+    }
+#pragma unroll
+    for (int t = 0; t < WL; ++t) {
+      const int e = tid + 256 * t, dd = e / (C / 4), c4 = e % (C / 4);
+      *reinterpret_cast<float4*>(&ws[dd][4 * c4]) = wv[t];
+    }
+    __syncthreads();
+#pragma unroll 2
+    for (int dd = 0; dd < dn; ++dd) {
+      float av[TR], bv[TC];
+#pragma unroll
+      for (int a = 0; a < TR; a += 4) {
+        const float4 a4 = *reinterpret_cast<const float4*>(&xs[dd][TR * tr + a]);
+        av[a] = a4.x;
+        av[a + 1] = a4.y;
+        av[a + 2] = a4.z;
+        av[a + 3] = a4.w;
+      }
+#pragma unroll
+      for (int c = 0; c < TC; c += 4) {
+        const float4 b4 = *reinterpret_cast<const float4*>(&ws[dd][TC * tc + c]);
+        bv[c] = b4.x;
+        bv[c + 1] = b4.y;
+        bv[c + 2] = b4.z;
+        bv[c + 3] = b4.w;
+      }
+#pragma unroll
+      for (int a = 0; a < TR; ++a)
+#pragma unroll
+        for (int c = 0; c < TC; ++c) acc[a][c] = __builtin_fmaf(av[a], bv[c], acc[a][c]);
+    }
+  }
+#pragma unroll
+  for (int a = 0; a < TR; ++a) {
+    const int64_t n = n0 + TR * tr + a;
+    if (n >= N) continue;
+#pragma unroll
+    for (int c = 0; c < TC; c += 4) {
+      const int j = j0 + TC * tc + c;
+      if (j < P)
+        *reinterpret_cast<float4*>(out + n * P + j) = float4{acc[a][c], acc[a][c + 1], acc[a][c + 2], acc[a][c + 3]};
+    }
+  }
+}
+
 // MaxSim scores over a tile of 16 query blocks x 64 key blocks: lane = key
 // block, wave = 4 query blocks (their prototype rows are LDS broadcasts).
 // Each score is the fmaf chain over e (in order, from 0) of q . k, maximised
@@ -710,6 +809,15 @@ extern "C" int spruce_gate_project(const float* x, const float* w, int64_t N, in
   SPRUCE_REQUIRE(N >= 1 && D >= 1 && P >= 1 && N * P < ((int64_t)1 << 40), "invalid projection shape");
   const bool vec = D % 4 == 0 && P % 4 == 0 && ((uintptr_t)x % 16) == 0 && ((uintptr_t)w % 16) == 0 &&
                    ((uintptr_t)out % 16) == 0;
+  if (vec && N >= kBlockProjectRows) {
+    constexpr int TR = kBlockProjectTR, TC = kBlockProjectTC;
+    const int64_t brows = (N + 16 * TR - 1) / (16 * TR);
+    SPRUCE_REQUIRE(brows < ((int64_t)1 << 31) && P < ((int64_t)1 << 20) && D < ((int64_t)1 << 20),
+                   "projection too large");
+    hipLaunchKernelGGL((project_block_kernel<TR, TC>), dim3((unsigned)brows, (unsigned)((P + 16 * TC - 1) / (16 * TC))),
+                       dim3(256), 0, (hipStream_t)stream, x, w, N, (int)D, (int)P, out);
+    return check_launch("project_block_kernel");
+  }
   if (vec) {
     const int64_t vrows = (N + kVR - 1) / kVR;
     SPRUCE_REQUIRE(vrows < ((int64_t)1 << 31) && P < ((int64_t)1 << 20) && D < ((int64_t)1 << 20),

@@ -56,10 +56,12 @@ def test_projection_scores_and_topk_are_bit_exact():
 
 
 @pytest.mark.parametrize("N,D,P", [(1, 4, 4), (65, 96, 36), (200, 256, 128), (130, 160, 68), (33, 6, 5),
-                                   (4096 * 8, 128, 128)])
+                                   (4096 * 8, 128, 128), (16384 + 77, 100, 68), (20000, 260, 36)])
 def test_projection_shapes_are_bit_exact(N, D, P):
     # Vector tiles (D % 4 == 0, P % 4 == 0: ragged rows and columns, two
-    # 128-wide slices of D) and the scalar form (D = 6, P = 5).
+    # 128-wide slices of D), the scalar form (D = 6, P = 5) and, from 16K
+    # rows, 8 x 4 register tiles (ragged last row tile, D not a multiple of
+    # the 32-dim slice, P not a multiple of the 64-column tile).
     gen = torch.Generator().manual_seed(N + D + P)
     x = torch.randn(N, D, generator=gen)
     W = torch.randn(D, P, generator=gen) * 0.1
