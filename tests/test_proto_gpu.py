@@ -77,6 +77,22 @@ def test_proto_pool_matches_oracle(dtype, B, H, G, L, d, block, P, layout):
         _same(_proto_pool_seq(avg, block, P), _oracle(x, G, block, P), "two-step")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_key_side_keeps_negative_zero(dtype):
+    # One head per group: tokens enter the tile unchanged (no averaging), so
+    # an outlier row holding -0.0 is emitted with its sign bits (value
+    # equality alone would not see a -0 -> +0 change).
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(1, 2, 128, 64, generator=g).to(dtype)
+    x[:, :, 9] = 40.0
+    x[:, :, 9, ::3] = -0.0
+    got = _proto_pool_seq(x.to(DEV), 64, 8).float().cpu().numpy()
+    exp = _oracle(x, 2, 64, 8)
+    _same(torch.from_numpy(got), exp, "values")
+    assert np.array_equal(np.signbit(got), np.signbit(exp))
+    assert np.signbit(got[0, :, 0, 1, ::3]).all()      # the planted row is prototype 1 of block 0
+
+
 def test_full_size_cfg3_one_group_and_invariants():
     print("cfg3 protos: generating inputs", flush=True)
     q, k, _ = workloads.qkv(0, 65536, 28, 4, 128, torch.bfloat16, use_rope=False, layout="bthd")
