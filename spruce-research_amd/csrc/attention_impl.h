@@ -505,12 +505,16 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     b = bg / p.Hkv;
     g = bg - b * p.Hkv;
   }
-  // Tile t of the row is query head t / 2, half t % 2; the capture form
-  // orders them half-major (t = half * G + head) so that each part holds
-  // every query head of its halves for the group average.
+  // In 8-wave workgroups whose parts split the 2G tiles evenly, tiles are
+  // half-major (t = half * G + head): the waves of a part share their query
+  // rows, and the capture form needs every query head of a half in one part
+  // for the group average (dense causal at cfg2: 7.07-7.13 -> 6.93-6.95 ms;
+  // block mask and CSR rows unchanged). Otherwise tile t is query head t / 2,
+  // half t % 2 (one head per part in the 2-wave single-head shape), and the
+  // spare waves of the last part are inactive.
   bool active;
   int hq, qhalf;
-  if constexpr (CAP) {
+  if (CAP || (WAVES == 8 && p.tpp * p.parts == 2 * p.G)) {
     const int t = part * p.tpp + wave;
     active = wave < p.tpp;
     qhalf = active ? t / p.G : 0;
