@@ -138,7 +138,7 @@ struct BlockIter<kModePadded> {
   const int32_t* row;
   int64_t stride;
   int n, pos, qb;
-  __device__ void init(const AttnParams& p, int b, int g, int qb_, int, int, int) {
+  __device__ void init(const AttnParams& p, int b, int g, int qb_, int, int, int, bool) {
     row = p.idx + (int64_t)b * p.is[0] + (int64_t)g * p.is[1] + (int64_t)qb_ * p.is[2];
     stride = p.is[3];
     n = p.K;
@@ -163,7 +163,7 @@ template <>
 struct BlockIter<kModeCsr> {
   const int32_t* row;
   int n, pos, qb;
-  __device__ void init(const AttnParams& p, int b, int g, int qb_, int, int, int) {
+  __device__ void init(const AttnParams& p, int b, int g, int qb_, int, int, int, bool) {
     const int64_t r = ((int64_t)b * p.Hkv + g) * p.Qb + qb_;
     int start = __builtin_amdgcn_readfirstlane(p.indptr[r]);
     int end = __builtin_amdgcn_readfirstlane(p.indptr[r + 1]);
@@ -192,7 +192,7 @@ struct BlockIter<kModeCsr> {
 template <>
 struct BlockIter<kModeCausal> {
   int pos, qb;
-  __device__ void init(const AttnParams&, int, int, int qb_, int, int, int) {
+  __device__ void init(const AttnParams&, int, int, int qb_, int, int, int, bool) {
     pos = 0;
     qb = qb_;
   }
@@ -207,42 +207,63 @@ struct BlockIter<kModeCausal> {
 // Mask rows are scanned 64 columns at a time with ballots; the bytes of the
 // next 64 columns are loaded one chunk ahead and kept raw, so the wait for
 // them falls where they are used (behind any key block loads issued later).
-constexpr int kMaxUnion = 5;  // query heads the tiles of one workgroup (<= 8 waves) can span
+//
+// With a per-query-head mask a workgroup walks the union of the mask rows of
+// the query heads its tiles belong to.  Those heads are the tile -> head map
+// of the kernel applied to the part's tiles [part * tpp, part * tpp + tpp):
+//   * half-major order (tile t = half * G + head): heads t mod G, a run of
+//     min(tpp, G) consecutive heads that may wrap past G - 1 to head 0;
+//   * head-major order (tile t = 2 * head + half): heads t / 2, a run of at
+//     most tpp / 2 + 1 heads that never wraps.
+// Both are a start head plus a count (<= 8 for parts of <= 8 tiles).
+constexpr int kMaxUnion = 8;
 
 template <>
 struct BlockIter<kModeMask> {
-  const uint8_t* base;  // row of the first head of the union
+  const uint8_t* base;  // mask row qb of query head 0 of the KV group
   int64_t hstride, cstride;
-  int nunion, own, qb, chunk, lane;
+  int hstart, G, nunion, own, qb, chunk, lane;
   uint64_t bits, ownbits;
   uint32_t raw[kMaxUnion];  // prefetched bytes of chunk `chunk` for this lane's column
   __device__ void fetch() {
     const int col = chunk * 64 + lane;
 #pragma unroll
-    for (int h = 0; h < kMaxUnion; ++h)
-      raw[h] = (h < nunion && col <= qb) ? base[(int64_t)h * hstride + (int64_t)col * cstride] : 0u;
+    for (int h = 0; h < kMaxUnion; ++h) {
+      int hh = hstart + h;
+      if (hh >= G) hh -= G;
+      raw[h] = (h < nunion && col <= qb) ? base[(int64_t)hh * hstride + (int64_t)col * cstride] : 0u;
+    }
   }
-  __device__ void init(const AttnParams& p, int b, int g, int qb_, int part, int hq, int lane_) {
+  __device__ void init(const AttnParams& p, int b, int g, int qb_, int part, int hq, int lane_, bool half_major) {
     cstride = p.ms[3];
     qb = qb_;
     lane = lane_;
     chunk = 0;
     bits = ownbits = 0;
     if (p.mask_per_qhead) {
-      // Union over the query heads whose tiles this workgroup owns.
-      const int t0 = part * p.tpp;
-      int t1 = t0 + p.tpp;
-      if (t1 > 2 * p.G) t1 = 2 * p.G;
-      const int h0 = t0 >> 1, h1 = (t1 - 1) >> 1;
-      base = p.mask + (int64_t)b * p.ms[0] + (int64_t)(g * p.G + h0) * p.ms[1] + (int64_t)qb_ * p.ms[2];
+      base = p.mask + (int64_t)b * p.ms[0] + (int64_t)(g * p.G) * p.ms[1] + (int64_t)qb_ * p.ms[2];
       hstride = p.ms[1];
-      nunion = h1 - h0 + 1;
-      own = hq - h0;
-      if (own < 0) own = 0;
+      G = p.G;
+      const int t0 = part * p.tpp;
+      if (half_major) {
+        hstart = t0 % p.G;
+        nunion = p.tpp < p.G ? p.tpp : p.G;
+      } else {
+        int t1 = t0 + p.tpp;
+        if (t1 > 2 * p.G) t1 = 2 * p.G;
+        hstart = t0 >> 1;
+        nunion = ((t1 - 1) >> 1) - hstart + 1;
+      }
+      if (nunion > kMaxUnion) nunion = kMaxUnion;  // not reached: parts hold <= 8 tiles
+      // Position of the wave's own head in the run (inactive waves: any).
+      own = hq - hstart;
+      if (own < 0) own += p.G;
       if (own >= nunion) own = nunion - 1;
     } else {
       base = p.mask + (int64_t)b * p.ms[0] + (int64_t)g * p.ms[1] + (int64_t)qb_ * p.ms[2];
       hstride = 0;
+      hstart = 0;
+      G = 1;
       nunion = 1;
       own = 0;
     }
@@ -508,13 +529,15 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
   // In 8-wave workgroups whose parts split the 2G tiles evenly, tiles are
   // half-major (t = half * G + head): the waves of a part share their query
   // rows, and the capture form needs every query head of a half in one part
-  // for the group average (dense causal at cfg2: 7.07-7.13 -> 6.93-6.95 ms;
-  // block mask and CSR rows unchanged). Otherwise tile t is query head t / 2,
-  // half t % 2 (one head per part in the 2-wave single-head shape), and the
-  // spare waves of the last part are inactive.
+  // for the group average (dense causal at cfg2: 7.07-7.13 -> 6.93-6.95 ms).
+  // Otherwise tile t is query head t / 2, half t % 2 (one head per part in
+  // the 2-wave single-head shape), and the spare waves of the last part are
+  // inactive.  The per-query-head mask walker derives the heads of a part
+  // from the same order.
+  const bool half_major = CAP || (WAVES == 8 && p.tpp * p.parts == 2 * p.G);
   bool active;
   int hq, qhalf;
-  if (CAP || (WAVES == 8 && p.tpp * p.parts == 2 * p.G)) {
+  if (half_major) {
     const int t = part * p.tpp + wave;
     active = wave < p.tpp;
     qhalf = active ? t / p.G : 0;
@@ -799,7 +822,7 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
   };
 
   BlockIter<MODE> it;
-  it.init(p, b, g, qb, part, hq, lane);
+  it.init(p, b, g, qb, part, hq, lane, half_major);
   int cur_id = 0;
   bool cur_en = false;
   int buf = 0;

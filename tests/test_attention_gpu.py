@@ -267,3 +267,99 @@ def test_full_size_cfg5_csr_sampled_rows():
     expected = ora.sparse_attention_csr(qs.numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(),
                                         indptr.numpy(), indices.numpy(), qblocks_subset=sample)
     _assert_parity(out[:, rows], expected[:, rows], what="cfg5 sampled rows")
+
+
+@pytest.mark.parametrize("variant", ["single_head", "single_head_qtile"])
+@pytest.mark.parametrize("Hq,Hkv", [
+    (28, 4),   # G=7, Qwen2-7B: two 8-wave parts of 7 tiles (half-major)
+    (20, 4),   # G=5
+    (24, 4),   # G=6
+    (32, 4),   # G=8: two full 8-wave parts (half-major)
+    (12, 4),   # G=3: one part, 6 tiles of 3 heads
+    (20, 2),   # G=10: 8-wave parts, head-major order
+    (24, 2),   # G=12: three 8-wave parts, the middle one wraps to head 0
+    (32, 2),   # G=16: four 8-wave parts
+])
+def test_mask_per_query_head_differs_within_group(Hq, Hkv, variant):
+    # Per-query-head masks whose heads differ inside each KV group: every
+    # part of a row must walk the mask rows of exactly the heads its tiles
+    # hold (reference kernels/seerattention_triton.py:41-68 reads
+    # mask[z, h, row, col] per head).
+    G = Hq // Hkv
+    rng = np.random.default_rng(Hq * 100 + Hkv)
+    B, T, D = 1, 700, 128
+    gen = torch.Generator().manual_seed(Hq + Hkv)
+    q = _bthd(B, T, Hq, D, torch.bfloat16, gen)
+    k = _bthd(B, T, Hkv, D, torch.bfloat16, gen)
+    v = _bthd(B, T, Hkv, D, torch.bfloat16, gen)
+    qblocks = (T + 63) // 64
+    mask = rng.random((B, Hq, qblocks, qblocks)) < 0.35
+    # Blocks that only the last head of each group selects, so a part that
+    # misses that head's row skips them.
+    for g in range(Hkv):
+        mask[:, g * G:(g + 1) * G - 1, :, 2] = False
+        mask[:, (g + 1) * G - 1, 2:, 2] = True
+    mask[0, 1, 4] = False   # one empty (head, row): zeros
+    expected = ora.sparse_attention_mask(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                         mask, empty="zero")
+    dev = [x.transpose(1, 2).contiguous().to(DEV).transpose(1, 2) for x in (q, k, v)]
+    actual = block_sparse_prefill(*dev, torch.from_numpy(mask).to(DEV), scale=D ** -0.5,
+                                  kernel_variant=variant)
+    _assert_parity(actual.transpose(1, 2), expected, what=f"per-head mask G={G} {variant}")
+
+
+def _ascending_route(rng, B, L, Hkv, qblocks, K):
+    """[B, L, Hkv, Qb, K] int32 rows: sink 0 and the diagonal always listed,
+    the rest a random causal subset, ascending, -1 padded."""
+    route = np.full((B, L, Hkv, qblocks, K), -1, np.int32)
+    for idx in np.ndindex(B, L, Hkv, qblocks):
+        qb = idx[-1]
+        extra = rng.permutation(np.arange(1, qb))[: rng.integers(0, K - 1)] if qb > 1 else []
+        row = sorted({0, qb, *map(int, extra)})[:K]
+        route[idx][: len(row)] = row
+    return route
+
+
+def test_route_adapters_on_device_feed_mask_and_index_kernels():
+    # kernels/sparse_prefill.py:16-52 in the reference: the route -> block
+    # mask and route -> per-query-head index adapters, run on device tensors
+    # and fed to the HIP kernels.
+    rng = np.random.default_rng(7)
+    from kernels.sparse_prefill import selected_blocks_to_block_mask, selected_blocks_to_head_indices
+    B, L, Hq, Hkv, T, D = 1, 2, 28, 4, 1000, 128
+    G = Hq // Hkv
+    qblocks = (T + 63) // 64
+    route = _ascending_route(rng, B, L, Hkv, qblocks, 6)
+    route_d = torch.from_numpy(route).to(DEV)
+    gen = torch.Generator().manual_seed(11)
+    q = _bthd(B, T, Hq, D, torch.bfloat16, gen)
+    k = _bthd(B, T, Hkv, D, torch.bfloat16, gen)
+    v = _bthd(B, T, Hkv, D, torch.bfloat16, gen)
+    dev = [x.transpose(1, 2).contiguous().to(DEV).transpose(1, 2) for x in (q, k, v)]
+
+    mask_d = selected_blocks_to_block_mask(route_d, layer_idx=1, num_query_heads=Hq)
+    heads_d = selected_blocks_to_head_indices(route_d, layer_idx=1, num_query_heads=Hq)
+    assert mask_d.is_cuda and heads_d.is_cuda
+    # The device adapters agree with the same adapters on the host.
+    assert torch.equal(mask_d.cpu(), selected_blocks_to_block_mask(
+        torch.from_numpy(route), layer_idx=1, num_query_heads=Hq))
+    assert torch.equal(heads_d.cpu(), selected_blocks_to_head_indices(
+        torch.from_numpy(route), layer_idx=1, num_query_heads=Hq))
+    assert mask_d.shape == (B, Hq, qblocks, qblocks) and heads_d.shape == (B, Hq, qblocks, 6)
+
+    by_mask = block_sparse_prefill(*dev, mask_d, scale=D ** -0.5).transpose(1, 2).contiguous()
+    by_index = direct_index_sparse_prefill(*dev, route_d[:, 1].contiguous(), scale=D ** -0.5)
+    # Per-query-head rows run against K/V expanded to the query heads (the
+    # reference's mask kernel takes expanded K/V the same way).
+    k_exp = dev[1].repeat_interleave(G, dim=1)
+    v_exp = dev[2].repeat_interleave(G, dim=1)
+    by_heads = direct_index_sparse_prefill(dev[0], k_exp, v_exp, heads_d, scale=D ** -0.5)
+    torch.cuda.synchronize()
+    expected = ora.sparse_attention_index(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                          route[:, 1])
+    _assert_parity(by_mask, expected, what="route -> mask")
+    _assert_parity(by_index, expected, what="route -> index (KV heads)")
+    _assert_parity(by_heads, expected, what="route -> per-query-head index")
+    # Identical ascending block sets give identical arithmetic per tile.
+    assert torch.equal(by_mask, by_index)
+    assert torch.equal(by_heads, by_index)
