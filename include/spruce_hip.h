@@ -380,6 +380,26 @@ int spruce_kv_summary(const void* k, const int64_t ks[4], const void* v, const i
                       size_t workspace_bytes, void* stream);
 
 /*
+ * spruce_kv_summary without a workspace argument and without any device
+ * allocation.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops that
+ * forbid hipMalloc).  The workspace is a library-held static device buffer of
+ * SPRUCE_KV_SUMMARY_NOALLOC_MAX_BYTES (64 MiB) per GPU, held from the first
+ * use of the library's summary kernels on that GPU until the process ends;
+ * shapes with spruce_kv_summary_workspace_bytes(B, Hkv, T, D) above it (for
+ * example B * Hkv * T > 4 * 65536 at D = 128) return SPRUCE_EINVAL.
+ * The current device must be the device of `stream`.  Every call on one GPU
+ * shares that buffer: calls that overlap on one GPU (concurrent streams or
+ * threads) race and must be serialised by the caller.  Results are identical
+ * to spruce_kv_summary's.
+ */
+#define SPRUCE_KV_SUMMARY_NOALLOC_MAX_BYTES (64u << 20)
+int spruce_kv_summary_noalloc(const void* k, const int64_t ks[4], const void* v, const int64_t vs[4], int64_t B,
+                              int64_t Hkv, int64_t T, int64_t D, int dtype, const uint8_t* valid,
+                              const int64_t* range_starts, const int64_t* range_ends, int64_t R, float* keys,
+                              float* values, float* counts, float* log_counts, void* stream);
+
+/*
  * Packs compact traversal IDs into selected_blocks rows.  Replaces
  * selected_ids_to_blocks (scripts/export_selected_blocks.py:79-175), same
  * policy: forced sink blocks [0, min(sink_blocks, key_blocks)) strictly before

@@ -22,6 +22,8 @@
 // range adds its covered chunks one by one.  HBM-bound: K and V are read once.
 #include <math.h>
 
+#include <mutex>
+
 #include "common.h"
 
 namespace spruce {
@@ -506,11 +508,17 @@ extern "C" size_t spruce_kv_summary_workspace_bytes(int64_t B, int64_t Hkv, int6
   return workspace_bytes(B, Hkv, T, D);
 }
 
-extern "C" int spruce_kv_summary(const void* k, const int64_t ks[4], const void* v, const int64_t vs[4], int64_t B,
-                                 int64_t Hkv, int64_t T, int64_t D, int dtype, const uint8_t* valid,
-                                 const int64_t* range_starts, const int64_t* range_ends, int64_t R, float* keys,
-                                 float* values, float* counts, float* log_counts, void* workspace,
-                                 size_t workspace_bytes_given, void* stream) {
+namespace spruce {
+namespace {
+
+// The body of spruce_kv_summary and spruce_kv_summary_noalloc: `workspace`
+// is caller memory or the library's static scratch.  Every workspace entry
+// is written by the first launches before any launch reads it, so it needs
+// no clearing between calls.
+int kv_summary_run(const void* k, const int64_t ks[4], const void* v, const int64_t vs[4], int64_t B, int64_t Hkv,
+                   int64_t T, int64_t D, int dtype, const uint8_t* valid, const int64_t* range_starts,
+                   const int64_t* range_ends, int64_t R, float* keys, float* values, float* counts,
+                   float* log_counts, void* workspace, size_t workspace_bytes_given, void* stream) {
   SPRUCE_REQUIRE(k && v && ks && vs && keys && values && counts && log_counts && workspace,
                  "tensors, strides and workspace must be non-null");
   SPRUCE_REQUIRE(range_starts && range_ends, "range tables must be non-null");
@@ -563,4 +571,78 @@ extern "C" int spruce_kv_summary(const void* k, const int64_t ks[4], const void*
   if (dtype == SPRUCE_DTYPE_BF16) return launch_dyadic_nk<InBF16>(pp, g2, (hipStream_t)stream);
   if (dtype == SPRUCE_DTYPE_F16) return launch_dyadic_nk<InF16>(pp, g2, (hipStream_t)stream);
   return launch_dyadic_nk<InF32>(pp, g2, (hipStream_t)stream);
+}
+
+}  // namespace
+}  // namespace spruce
+
+extern "C" int spruce_kv_summary(const void* k, const int64_t ks[4], const void* v, const int64_t vs[4], int64_t B,
+                                 int64_t Hkv, int64_t T, int64_t D, int dtype, const uint8_t* valid,
+                                 const int64_t* range_starts, const int64_t* range_ends, int64_t R, float* keys,
+                                 float* values, float* counts, float* log_counts, void* workspace,
+                                 size_t workspace_bytes_given, void* stream) {
+  return kv_summary_run(k, ks, v, vs, B, Hkv, T, D, dtype, valid, range_starts, range_ends, R, keys, values, counts,
+                        log_counts, workspace, workspace_bytes_given, stream);
+}
+
+// ------------------------------------------------------- allocation-free form
+// The workspace of spruce_kv_summary_noalloc: one copy per GPU, created when
+// the library's code object is loaded on that GPU and held until the process
+// ends.  Host code never uses this name as an address (on the host it is a
+// stand-in symbol): the device address comes from hipGetSymbolAddress, looked
+// up once per device with that device current.
+static __device__ __align__(256) unsigned char scratch[SPRUCE_KV_SUMMARY_NOALLOC_MAX_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, which must be the
+// device of `stream` (a stream of another device would run the kernels where
+// this address is not mapped).
+int scratch_for_stream(void* stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return spruce::set_error((int)e, "hipGetDevice failed: %s", hipGetErrorString(e));
+  SPRUCE_REQUIRE(dev >= 0 && dev < kMaxDevices, "device %d outside the %d devices supported", dev, kMaxDevices);
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice((hipStream_t)stream, &sdev);
+    if (e != hipSuccess) return spruce::set_error((int)e, "hipStreamGetDevice failed: %s", hipGetErrorString(e));
+    SPRUCE_REQUIRE(sdev == dev, "stream belongs to device %d but device %d is current", (int)sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return spruce::set_error(e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol,
+                               "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int spruce_kv_summary_noalloc(const void* k, const int64_t ks[4], const void* v, const int64_t vs[4],
+                                         int64_t B, int64_t Hkv, int64_t T, int64_t D, int dtype,
+                                         const uint8_t* valid, const int64_t* range_starts,
+                                         const int64_t* range_ends, int64_t R, float* keys, float* values,
+                                         float* counts, float* log_counts, void* stream) {
+  SPRUCE_REQUIRE(B >= 1 && Hkv >= 1 && T >= 1 && D >= 1, "invalid shape");
+  SPRUCE_REQUIRE(B < (1 << 20) && Hkv < (1 << 16) && T < ((int64_t)1 << 30) && D <= 4096, "shape out of range");
+  const size_t need = workspace_bytes(B, Hkv, T, D);
+  SPRUCE_REQUIRE(need <= (size_t)SPRUCE_KV_SUMMARY_NOALLOC_MAX_BYTES,
+                 "spruce_kv_summary_noalloc: this shape needs %zu bytes of scratch, above its limit of %zu bytes "
+                 "(use spruce_kv_summary with a caller workspace)",
+                 need, (size_t)SPRUCE_KV_SUMMARY_NOALLOC_MAX_BYTES);
+  void* ws = nullptr;
+  const int rc = scratch_for_stream(stream, &ws);
+  if (rc) return rc;
+  return kv_summary_run(k, ks, v, vs, B, Hkv, T, D, dtype, valid, range_starts, range_ends, R, keys, values, counts,
+                        log_counts, ws, (size_t)SPRUCE_KV_SUMMARY_NOALLOC_MAX_BYTES, stream);
 }

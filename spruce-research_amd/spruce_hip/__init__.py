@@ -63,6 +63,9 @@ _SIGNATURES = {
     "spruce_kv_summary": [
         _p, _STRIDES, _p, _STRIDES, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _p, _p, _i64,
         _p, _p, _p, _p, _p, ctypes.c_size_t, _p],
+    "spruce_kv_summary_noalloc": [
+        _p, _STRIDES, _p, _STRIDES, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _p, _p, _i64,
+        _p, _p, _p, _p, _p],
     "spruce_group_avg_tokens": [_p, _STRIDES, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _p],
     "spruce_sparse_prefill_index_summaries": [
         _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _i64,
