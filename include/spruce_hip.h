@@ -295,16 +295,34 @@ int spruce_gate_candidate_scores(const float* qp, const float* kp, const int32_t
  * Teacher target extraction.
  * ---------------------------------------------------------------------- */
 
+/* Schedules of the teacher block mass (a row's mass needs its final softmax
+ * denominator before its rows are summed):
+ *   SPRUCE_TEACHER_SCRATCH  single pass; each row's per-key-block partial
+ *                           sum and reference point (8 bytes per row and key
+ *                           block) go to the workspace, while they take at
+ *                           most 4 GiB (T <= 32K at 28 query heads);
+ *   SPRUCE_TEACHER_TWO_PASS row statistics, then QK^T again for the mass.
+ * SPRUCE_TEACHER_AUTO takes the single pass when it applies and the
+ * workspace holds it.  Both write per-half tile partials [B, Hq, 2, Qb, Qb]
+ * float32 to the workspace and add the two halves into mass. */
+#define SPRUCE_TEACHER_AUTO 0
+#define SPRUCE_TEACHER_SCRATCH 1
+#define SPRUCE_TEACHER_TWO_PASS 2
+
 /* Device workspace of spruce_teacher_block_mass, Qb = ceil(T/64).
- * _min: the two-pass schedule -- row statistics [B, Hq, T, 2] plus per-half
- *   tile partials [B, Hq, 2, Qb, Qb] float32; QK^T is computed twice.
- * spruce_teacher_workspace_bytes: the preferred size.  While
- *   B*Hq*Qb*(Qb+1)*256 <= 4 GiB it adds the single-pass scratch (each row's
- *   per-key-block partial sum and reference max, 8 bytes per row and block)
- *   and a workspace of at least this size selects the single pass, which
- *   computes QK^T once; otherwise it equals _min. */
+ * _min: the two-pass schedule -- row statistics [B, Hq, T, 2] plus the
+ *   tile partials.
+ * spruce_teacher_workspace_bytes: enough for every schedule (the scratch
+ *   schedule's partials included while they take at most 4 GiB).
+ * spruce_teacher_schedule_workspace_bytes: what one schedule needs.
+ * spruce_teacher_schedule: the schedule SPRUCE_TEACHER_AUTO takes for this
+ *   shape given workspace_bytes of workspace (SIZE_MAX: unlimited), or
+ *   SPRUCE_EINVAL for an invalid shape.
+ * These are the ABI's own sizing helpers (no reference counterpart). */
 size_t spruce_teacher_workspace_bytes(int64_t B, int64_t Hq, int64_t T);
 size_t spruce_teacher_workspace_bytes_min(int64_t B, int64_t Hq, int64_t T);
+size_t spruce_teacher_schedule_workspace_bytes(int64_t B, int64_t Hq, int64_t T, int schedule);
+int spruce_teacher_schedule(int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D, size_t workspace_bytes);
 
 /*
  * Dense causal softmax attention reduced to block probability mass without
@@ -316,11 +334,17 @@ size_t spruce_teacher_workspace_bytes_min(int64_t B, int64_t Hq, int64_t T);
  *   q [B, Hq, T, D], k [B, Hkv, T, D] (strides as for the attention entry
  *   points), mass float32 [B, Hq, Qb, Qb] contiguous, D in {64, 128}.
  * Rows of mass sum to the number of real query rows of the block (64).
+ * The _schedule form takes one of the SPRUCE_TEACHER_* schedules (an
+ * inapplicable one is SPRUCE_EINVAL); the plain form is SPRUCE_TEACHER_AUTO.
  */
 int spruce_teacher_block_mass(const void* q, const int64_t qs[4], const void* k, const int64_t ks[4],
                               int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D, float scale,
                               int dtype, float* mass, float* workspace, size_t workspace_bytes,
                               void* stream);
+int spruce_teacher_block_mass_schedule(const void* q, const int64_t qs[4], const void* k, const int64_t ks[4],
+                                       int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D, float scale,
+                                       int dtype, float* mass, float* workspace, size_t workspace_bytes,
+                                       int schedule, void* stream);
 
 /*
  * Teacher targets from block mass (load_teacher, selector/targets.py:104-121,

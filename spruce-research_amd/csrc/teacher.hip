@@ -11,26 +11,38 @@
 // KV group, causal mask, row normalisation with eps, plus the top-k blocks of
 // each target row (selector/loss.py:34-46, selector/recall.py:35).
 //
-// Scores are computed in float32 from bf16/f16 MFMA inputs (the reference
-// rounds QK^T to the model dtype before its float32 softmax,
-// teacher/chunked_extract.py:119,126).
+// Scores are accumulated in float32 on the matrix cores from the bf16/f16
+// inputs as given (the reference rounds QK^T itself to the model dtype
+// before its float32 softmax, teacher/chunked_extract.py:119,126).  Q is not
+// prescaled: rounding q * scale * log2(e) to bf16 would add a score error
+// that grows with the score's magnitude.
 //
 // The causal (I, J) tiles are walked GQA-packed like the sparse prefill
 // kernel (one workgroup per (batch, KV head, query block, part), one 32-row
 // tile of one query head per wave, K blocks staged once per workgroup in LDS).
+//
+// Per score element the loop issues one FMA (s * cs - m, cs = scale *
+// log2(e)), one v_exp_f32 and one add; the row max is taken only in the rare
+// blocks whose partial sum exceeds kMassCheckSum, not per block.  On gfx950
+// v_exp_f32 issues at half the rate of an FMA and does not overlap other VALU
+// work, so per element these three already take about as long as the MFMA
+// work of the score; any further VALU work per element shows in the time.
+//
 // A row's mass needs its final softmax denominator l before its 64 rows are
 // summed, so one of two schedules is used:
 //   single pass (when its scratch fits, see kSinglePassScratchMax): online
-//     row max / denominator as in attention, and for every J the row's
-//     partial sum e_J = sum_j exp2(s_j - m_J) with its reference point m_J
-//     written to scratch (8 bytes per row and J); once the row is complete
-//     the wave reads them back and sums e_J * exp2(m_J - m) / l over its 32
-//     rows in a fixed butterfly order.  QK^T runs once.
-//   two passes (longer sequences): pass 1 keeps only the row max and
-//     denominator; pass 2 recomputes the scores and sums exp(s - m) / l over
-//     each 32-row x 64-key tile.  QK^T runs twice.
+//     row reference point and denominator, and for every J the row's partial
+//     sum e_J = sum_j exp2(s_j - m_J) with its reference point m_J written to
+//     scratch (8 bytes per row and J); once the row is complete the wave
+//     reads them back and sums e_J * exp2(m_J - m) / l over its 32 rows in a
+//     fixed butterfly order.  QK^T runs once.
+//   two passes (longer sequences): pass 1 keeps only the row reference point
+//     and denominator; pass 2 recomputes the scores and sums exp2(s - m) / l
+//     over each 32-row x 64-key tile.  QK^T runs twice.
 // Both write one float per (tile half, J) into a [B, H, 2, Qb, Qb] workspace;
 // mass = half0 + half1 (exactly two addends, order-independent).
+#include <type_traits>
+
 #include "attention_impl.h"
 
 namespace spruce {
@@ -55,6 +67,13 @@ inline int64_t single_pass_scratch_bytes(int64_t B, int64_t Hq, int64_t Qb) {
   return B * Hq * Qb * (Qb + 1) * 256;
 }
 
+// A half-row block sum above this triggers the max check (the row's
+// reference point is raised only when the block max exceeds it by more than
+// kRescaleThreshold).
+constexpr float kMassCheckSum = 256.0f;
+
+// PASS 1: row statistics; PASS 2: tile mass from them; PASS 3: single pass
+// with per-row partials in the workspace.
 template <int D, int WAVES, typename TIn, bool F16, int PASS>
 __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams p) {
   constexpr int NTHR = WAVES * 64;
@@ -90,7 +109,6 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
   const int q0 = qb * kBlock + half * 32;
   const int qin = half * 32 + l32;
   const int qtok = q0 + l32;
-
   uint4 qf[KS];
   {
     const int qrs = (int)(p.qs[2] * EB);
@@ -128,8 +146,9 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
         *reinterpret_cast<uint4*>(Ks + klds0 + i * KRP * KSTR) = raw_to_mfma<TIn, F16>(kst[i]);
   };
 
-  // Row statistics (pass 1 accumulates them; pass 2 reads them).
-  float m_use = -INFINITY, l_run = 0.f, inv_l = 0.f;
+  // Row statistics in log2 units: m_use is the reference point, l_run the
+  // running sum relative to it (pass 1 and 3 build them; pass 2 reads them).
+  float m_use = 0.f, l_run = 0.f, inv_l = 0.f;
   float* stat = p.stats + (((int64_t)b * p.Hq + head) * p.T + (qtok < p.T ? qtok : 0)) * 2;
   if (PASS == 2 && active && qtok < p.T) {
     m_use = stat[0];
@@ -142,78 +161,91 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
     rowj = p.rowj + ((((int64_t)b * p.Hq + head) * 2 + half) * ((int64_t)p.Qb * (p.Qb + 1) / 2) +
                      (int64_t)qb * (qb + 1) / 2) * 32;
 
-  load_k(0);
-  store_k(0);
-  __syncthreads();
-  int buf = 0;
-  for (int J = 0; J <= qb; ++J) {
-    const bool more = J < qb;
-    if (more) load_k(J + 1);
-    if (active) {
-      const uint16_t* kp = smem + buf * KTILE + l32 * KSTR + 8 * hl;
-      f32x16_t s0 = f32x16_t{}, s1 = f32x16_t{};
-      uint4 a0 = *reinterpret_cast<const uint4*>(kp);
-      uint4 a1 = *reinterpret_cast<const uint4*>(kp + 32 * KSTR);
+  // One block of the row: S^T = K Q^T (from the reference point), the
+  // exponentials, the row-statistics update (PASS 1/3) and the partial
+  // (PASS 3) or tile mass (PASS 2).  The diagonal block (last) is the only
+  // one with a causal mask, so it runs as its own instance.
+  auto step = [&](auto diag_tag, int J, int buf) {
+    constexpr bool DIAG = decltype(diag_tag)::value;
+    const uint16_t* kp = smem + buf * KTILE + l32 * KSTR + 8 * hl;
+    f32x16_t s0 = f32x16_t{}, s1 = f32x16_t{};
+    uint4 a0 = *reinterpret_cast<const uint4*>(kp);
+    uint4 a1 = *reinterpret_cast<const uint4*>(kp + 32 * KSTR);
 #pragma unroll
-      for (int kk = 0; kk < KS; ++kk) {
-        uint4 n0 = a0, n1 = a1;
-        if (kk + 1 < KS) {
-          n0 = *reinterpret_cast<const uint4*>(kp + 16 * (kk + 1));
-          n1 = *reinterpret_cast<const uint4*>(kp + 32 * KSTR + 16 * (kk + 1));
-        }
-        s0 = mfma32x32x16<F16>(a0, qf[kk], s0);
-        s1 = mfma32x32x16<F16>(a1, qf[kk], s1);
-        a0 = n0;
-        a1 = n1;
+    for (int kk = 0; kk < KS; ++kk) {
+      uint4 n0 = a0, n1 = a1;
+      if (kk + 1 < KS) {
+        n0 = *reinterpret_cast<const uint4*>(kp + 16 * (kk + 1));
+        n1 = *reinterpret_cast<const uint4*>(kp + 32 * KSTR + 16 * (kk + 1));
       }
-      if (J == qb) {
-        const int thr = qin - 4 * hl;
+      s0 = mfma32x32x16<F16>(a0, qf[kk], s0);
+      s1 = mfma32x32x16<F16>(a1, qf[kk], s1);
+      a0 = n0;
+      a1 = n1;
+    }
+    if constexpr (DIAG) {
+      // Register r of key tile c holds key 32c + 8(r/4) + 4(lane/32) + r%4.
+      const int thr = qin - 4 * hl;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kr = 8 * (r >> 2) + (r & 3);
-          if (kr > thr) s0[r] = -INFINITY;
-          if (32 + kr > thr) s1[r] = -INFINITY;
-        }
+      for (int r = 0; r < 16; ++r) {
+        const int kr = 8 * (r >> 2) + (r & 3);
+        if (kr > thr) s0[r] = -INFINITY;
+        if (32 + kr > thr) s1[r] = -INFINITY;
       }
-      if (PASS == 1 || PASS == 3) {
+    }
+    // x = exp2(s * cs - m_use).  The sum starts from the first pair: adding
+    // it to +0.0 would cost an add per element (x + 0.0 is not x for
+    // x = -0.0, so the compiler keeps it).
+    const float cs = p.cs, nm = -m_use;
+    float ps = fast_exp2(fmaf(s0[0], cs, nm)) + fast_exp2(fmaf(s1[0], cs, nm));
+#pragma unroll
+    for (int r = 1; r < 16; ++r) ps += fast_exp2(fmaf(s0[r], cs, nm)) + fast_exp2(fmaf(s1[r], cs, nm));
+    if (PASS == 1 || PASS == 3) {
+      // Block 0 sets the reference point; later blocks only check their
+      // sum (NaN / inf included) and take the max when it is large.
+      if (__ballot(J == 0 || !(ps <= kMassCheckSum)) != 0) {
         float mx = fmaxf(s0[0], s0[1]);
 #pragma unroll
         for (int r = 2; r < 16; ++r) mx = fmaxf(mx, s0[r]);
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s1[r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float cand = mx * p.cs;
-        if (__ballot(cand > m_use + kRescaleThreshold) != 0) {
-          const float m_new = fmaxf(m_use, cand);
-          l_run *= fast_exp2(m_use - m_new);
-          m_use = m_new;
+        mx = fmaf(fmaxf(mx, __shfl_xor(mx, 32)), cs, nm);  // relative to m_use
+        const float delta = (J == 0 || mx > kRescaleThreshold) ? mx : 0.f;
+        if (__ballot(delta != 0.f) != 0) {
+          m_use += delta;
+          l_run *= fast_exp2(-delta);
+          const float nm2 = -m_use;
+          ps = fast_exp2(fmaf(s0[0], cs, nm2)) + fast_exp2(fmaf(s1[0], cs, nm2));
+#pragma unroll
+          for (int r = 1; r < 16; ++r) ps += fast_exp2(fmaf(s0[r], cs, nm2)) + fast_exp2(fmaf(s1[r], cs, nm2));
         }
-        const float nm = -m_use;
-        float ps = 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) ps += fast_exp2(fmaf(s0[r], p.cs, nm)) + fast_exp2(fmaf(s1[r], p.cs, nm));
-        l_run += ps;
-        if (PASS == 3) {
-          const float e = ps + __shfl_xor(ps, 32);
-          if (hl == 0) rowj[(int64_t)J * 32 + l32] = float2{e, m_use};
-        }
-      } else {
-        const float nm = -m_use;
-        float ps = 0.f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) ps += fast_exp2(fmaf(s0[r], p.cs, nm)) + fast_exp2(fmaf(s1[r], p.cs, nm));
-        float v = (qtok < p.T) ? ps * inv_l : 0.f;
-        // Sum over the wave's 32 query rows x 64 keys (fixed butterfly order).
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-        if (lane == 0) part_out[J] = v;
       }
+      l_run += ps;
+      if (PASS == 3) {
+        const float e = ps + __shfl_xor(ps, 32);
+        if (hl == 0) rowj[(int64_t)J * 32 + l32] = float2{e, m_use};
+      }
+    } else {
+      float v = (qtok < p.T) ? ps * inv_l : 0.f;
+      // Sum over the wave's 32 query rows x 64 keys (fixed butterfly order).
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+      if (lane == 0) part_out[J] = v;
     }
-    if (!more) break;
+  };
+
+  load_k(0);
+  store_k(0);
+  __syncthreads();
+  int buf = 0;
+  for (int J = 0; J < qb; ++J) {
+    load_k(J + 1);
+    if (active) step(std::false_type{}, J, buf);
     store_k(buf ^ 1);
     __syncthreads();
     buf ^= 1;
   }
+  if (active) step(std::true_type{}, qb, buf);
   if (PASS == 1 && active) {
     const float lt = l_run + __shfl_xor(l_run, 32);
     if (hl == 0 && qtok < p.T) {
@@ -395,6 +427,20 @@ int launch_mass_w(const MassParams& p, int waves, hipStream_t s) {
   return check_launch("block_mass_kernel");
 }
 
+// Bytes of the per-half tile partials [B, Hq, 2, Qb, Qb] float32, 256-byte rounded.
+inline size_t part_bytes(int64_t B, int64_t Hq, int64_t Qb) {
+  return ((size_t)B * Hq * 2 * Qb * Qb * sizeof(float) + 255) / 256 * 256;
+}
+
+// Workspace of each schedule.
+inline size_t schedule_workspace_bytes(int64_t B, int64_t Hq, int64_t T, int schedule) {
+  const int64_t Qb = (T + kBlock - 1) / kBlock;
+  switch (schedule) {
+    case SPRUCE_TEACHER_SCRATCH: return part_bytes(B, Hq, Qb) + (size_t)single_pass_scratch_bytes(B, Hq, Qb);
+    default: return (size_t)(B * Hq * T * 2 + B * Hq * 2 * Qb * Qb) * sizeof(float);
+  }
+}
+
 template <int PASS>
 int launch_mass(const MassParams& p, int D, int dtype, int waves, hipStream_t s) {
   if (D == 128) {
@@ -411,10 +457,24 @@ int launch_mass(const MassParams& p, int D, int dtype, int waves, hipStream_t s)
 
 using namespace spruce;
 
-extern "C" int spruce_teacher_block_mass(const void* q, const int64_t qs[4], const void* k, const int64_t ks[4],
-                                         int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D, float scale,
-                                         int dtype, float* mass, float* workspace, size_t workspace_bytes,
-                                         void* stream) {
+namespace {
+
+// Schedule of the auto mode: the single pass when its scratch is at most
+// kSinglePassScratchMax and the workspace holds it, else two passes.
+int pick_schedule(int64_t B, int64_t Hq, int64_t T, size_t workspace_bytes) {
+  const int64_t Qb = (T + kBlock - 1) / kBlock;
+  if (single_pass_scratch_bytes(B, Hq, Qb) <= kSinglePassScratchMax &&
+      workspace_bytes >= schedule_workspace_bytes(B, Hq, T, SPRUCE_TEACHER_SCRATCH))
+    return SPRUCE_TEACHER_SCRATCH;
+  return SPRUCE_TEACHER_TWO_PASS;
+}
+
+}  // namespace
+
+extern "C" int spruce_teacher_block_mass_schedule(const void* q, const int64_t qs[4], const void* k,
+                                                  const int64_t ks[4], int64_t B, int64_t Hq, int64_t Hkv, int64_t T,
+                                                  int64_t D, float scale, int dtype, float* mass, float* workspace,
+                                                  size_t workspace_bytes, int schedule, void* stream) {
   // Reuse the attention argument checks (v aliases k; out only needs alignment).
   AttnParams ap;
   LaunchShape shape;
@@ -423,10 +483,16 @@ extern "C" int spruce_teacher_block_mass(const void* q, const int64_t qs[4], con
                              mass, fake_os, shape);
   if (rc) return rc;
   SPRUCE_REQUIRE(mass != nullptr && workspace != nullptr, "mass and workspace must be non-null");
-  const int64_t Qb = (T + kBlock - 1) / kBlock;
-  const size_t need = spruce_teacher_workspace_bytes_min(B, Hq, T);
-  SPRUCE_REQUIRE(workspace_bytes >= need, "workspace too small: %zu bytes, need %zu", workspace_bytes, need);
+  SPRUCE_REQUIRE(schedule >= SPRUCE_TEACHER_AUTO && schedule <= SPRUCE_TEACHER_TWO_PASS, "unknown schedule %d",
+                 schedule);
   SPRUCE_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, "workspace must be 16-byte aligned");
+  const int64_t Qb = (T + kBlock - 1) / kBlock;
+  if (schedule == SPRUCE_TEACHER_AUTO) schedule = pick_schedule(B, Hq, T, workspace_bytes);
+  if (schedule == SPRUCE_TEACHER_SCRATCH)
+    SPRUCE_REQUIRE(single_pass_scratch_bytes(B, Hq, Qb) <= kSinglePassScratchMax,
+                   "the scratch schedule needs more than %lld bytes of scratch", (long long)kSinglePassScratchMax);
+  const size_t need = schedule_workspace_bytes(B, Hq, T, schedule);
+  SPRUCE_REQUIRE(workspace_bytes >= need, "workspace too small: %zu bytes, need %zu", workspace_bytes, need);
   MassParams p{};
   p.q = q;
   p.k = k;
@@ -444,12 +510,10 @@ extern "C" int spruce_teacher_block_mass(const void* q, const int64_t qs[4], con
   p.tpp = shape.tpp;
   p.cs = scale * 1.4426950408889634f;
   hipStream_t s = (hipStream_t)stream;
-  const int64_t scratch = single_pass_scratch_bytes(B, Hq, Qb);
-  if (scratch <= kSinglePassScratchMax && workspace_bytes >= spruce_teacher_workspace_bytes(B, Hq, T)) {
+  if (schedule == SPRUCE_TEACHER_SCRATCH) {
     // [part: B*Hq*2*Qb*Qb floats][rowj: scratch bytes], rowj 256-byte aligned.
     p.part = workspace;
-    const size_t part_bytes = ((size_t)B * Hq * 2 * Qb * Qb * sizeof(float) + 255) / 256 * 256;
-    p.rowj = reinterpret_cast<float2*>(reinterpret_cast<char*>(workspace) + part_bytes);
+    p.rowj = reinterpret_cast<float2*>(reinterpret_cast<char*>(workspace) + part_bytes(B, Hq, Qb));
     rc = launch_mass<3>(p, (int)D, dtype, shape.waves, s);
     if (rc) return rc;
   } else {
@@ -466,17 +530,37 @@ extern "C" int spruce_teacher_block_mass(const void* q, const int64_t qs[4], con
   return check_launch("mass_combine_kernel");
 }
 
+extern "C" int spruce_teacher_block_mass(const void* q, const int64_t qs[4], const void* k, const int64_t ks[4],
+                                         int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D, float scale,
+                                         int dtype, float* mass, float* workspace, size_t workspace_bytes,
+                                         void* stream) {
+  return spruce_teacher_block_mass_schedule(q, qs, k, ks, B, Hq, Hkv, T, D, scale, dtype, mass, workspace,
+                                            workspace_bytes, SPRUCE_TEACHER_AUTO, stream);
+}
+
+extern "C" int spruce_teacher_schedule(int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D,
+                                       size_t workspace_bytes) {
+  SPRUCE_REQUIRE(B >= 1 && Hkv >= 1 && Hq >= Hkv && Hq % Hkv == 0 && T >= 1 && (D == 64 || D == 128),
+                 "invalid shape");
+  return pick_schedule(B, Hq, T, workspace_bytes);
+}
+
+extern "C" size_t spruce_teacher_schedule_workspace_bytes(int64_t B, int64_t Hq, int64_t T, int schedule) {
+  if (B < 1 || Hq < 1 || T < 1) return 0;
+  if (schedule == SPRUCE_TEACHER_AUTO) {
+    const int64_t Qb = (T + kBlock - 1) / kBlock;
+    schedule = single_pass_scratch_bytes(B, Hq, Qb) <= kSinglePassScratchMax ? SPRUCE_TEACHER_SCRATCH
+                                                                               : SPRUCE_TEACHER_TWO_PASS;
+  }
+  return schedule_workspace_bytes(B, Hq, T, schedule);
+}
+
 extern "C" size_t spruce_teacher_workspace_bytes_min(int64_t B, int64_t Hq, int64_t T) {
-  const int64_t Qb = (T + kBlock - 1) / kBlock;
-  return (size_t)(B * Hq * T * 2 + B * Hq * 2 * Qb * Qb) * sizeof(float);
+  return schedule_workspace_bytes(B, Hq, T, SPRUCE_TEACHER_TWO_PASS);
 }
 
 extern "C" size_t spruce_teacher_workspace_bytes(int64_t B, int64_t Hq, int64_t T) {
-  const int64_t Qb = (T + kBlock - 1) / kBlock;
-  const int64_t scratch = single_pass_scratch_bytes(B, Hq, Qb);
-  if (scratch <= kSinglePassScratchMax)
-    return ((size_t)B * Hq * 2 * Qb * Qb * sizeof(float) + 255) / 256 * 256 + (size_t)scratch;
-  return spruce_teacher_workspace_bytes_min(B, Hq, T);
+  return spruce_teacher_schedule_workspace_bytes(B, Hq, T, SPRUCE_TEACHER_AUTO);
 }
 
 extern "C" int spruce_teacher_targets(const float* mass, int64_t B, int64_t Hq, int64_t Hkv, int64_t Qb, int64_t Kb,

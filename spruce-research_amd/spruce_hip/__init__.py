@@ -55,6 +55,10 @@ _SIGNATURES = {
     "spruce_teacher_block_mass": [
         _p, _STRIDES, _p, _STRIDES, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int,
         _p, _p, ctypes.c_size_t, _p],
+    "spruce_teacher_block_mass_schedule": [
+        _p, _STRIDES, _p, _STRIDES, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int,
+        _p, _p, ctypes.c_size_t, ctypes.c_int, _p],
+    "spruce_teacher_schedule": [_i64, _i64, _i64, _i64, _i64, ctypes.c_size_t],
     "spruce_teacher_targets": [
         _p, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _p, _p, _p, _p],
     "spruce_pack_selected_ids": [_p, ctypes.c_int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
@@ -82,6 +86,8 @@ _SIGNATURES = {
         _p, _STRIDES, _p],
 }
 
+SIZE_MAX = ctypes.c_size_t(-1).value
+
 _lib = None
 
 
@@ -107,6 +113,8 @@ def lib():
         for name in ("spruce_teacher_workspace_bytes", "spruce_teacher_workspace_bytes_min"):
             getattr(handle, name).restype = ctypes.c_size_t
             getattr(handle, name).argtypes = [_i64, _i64, _i64]
+        handle.spruce_teacher_schedule_workspace_bytes.restype = ctypes.c_size_t
+        handle.spruce_teacher_schedule_workspace_bytes.argtypes = [_i64, _i64, _i64, ctypes.c_int]
         handle.spruce_kv_summary_workspace_bytes.restype = ctypes.c_size_t
         handle.spruce_kv_summary_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64]
         _lib = handle

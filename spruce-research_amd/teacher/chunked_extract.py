@@ -7,9 +7,9 @@ pool_attention(causal_softmax(q k^T * scaling)).  ``key`` may be repeated to H
 heads as the reference passes it, or stay at native KV resolution
 ``[b, Hkv, k, d]`` (query head h reads KV head h // (H / Hkv)) -- no GQA copy
 is needed.  One HIP kernel computes QK^T once per causal tile (online row
-statistics plus per-row partial sums in a scratch workspace, combined once
-each row is complete); sequences whose scratch would exceed 4 GiB use two
-passes (row statistics, then recomputed tile mass).  ``head_chunk`` is
+statistics plus per-row partial sums of every key block in a workspace,
+combined once each row is complete); sequences whose workspace partials would
+exceed 4 GiB use two passes (row statistics, then recomputed tile mass).  ``head_chunk`` is
 accepted for signature compatibility and ignored (nothing is materialised
 per head).
 
@@ -37,11 +37,15 @@ def chunked_pool(query, key, scaling, block_size=_BLOCK, head_chunk=None):
     return block_mass(query, key, scaling, block_size=block_size)
 
 
+_SCHEDULES = {"auto": 0, "scratch": 1, "two_pass": 2}
+
+
 def block_mass(query, key, scaling, block_size=_BLOCK, schedule="auto"):
-    """chunked_pool's computation; ``schedule`` "auto" (single pass when its
-    scratch fits), or "two_pass" (the minimal workspace)."""
-    if schedule not in ("auto", "two_pass"):
-        raise ValueError(f"schedule must be 'auto' or 'two_pass', got {schedule!r}")
+    """chunked_pool's computation.  ``schedule``: "auto" (the single pass
+    when its workspace partials take at most 4 GiB), "scratch" (single pass)
+    or "two_pass"."""
+    if schedule not in _SCHEDULES:
+        raise ValueError(f"schedule must be one of {tuple(_SCHEDULES)}, got {schedule!r}")
     if block_size != _BLOCK:
         raise ValueError("the HIP block-mass kernel requires block_size=64")
     if not query.is_cuda:
@@ -58,15 +62,18 @@ def block_mass(query, key, scaling, block_size=_BLOCK, schedule="auto"):
     Hkv = key.shape[1]
     qb = (q_len + _BLOCK - 1) // _BLOCK
     mass = torch.empty((b, H, qb, qb), device=query.device, dtype=torch.float32)
-    size_fn = (spruce_hip.lib().spruce_teacher_workspace_bytes if schedule == "auto"
-               else spruce_hip.lib().spruce_teacher_workspace_bytes_min)
-    nbytes = size_fn(b, H, q_len)
-    ws = torch.empty(nbytes // 4, device=query.device, dtype=torch.float32)
+    lib = spruce_hip.lib()
+    code = _SCHEDULES[schedule]
+    if code == 0:
+        code = lib.spruce_teacher_schedule(b, H, Hkv, q_len, d, spruce_hip.SIZE_MAX)
+        spruce_hip.check(code if code < 0 else 0, "spruce_teacher_schedule")
+    nbytes = lib.spruce_teacher_schedule_workspace_bytes(b, H, q_len, code)
+    ws = torch.empty((nbytes + 3) // 4, device=query.device, dtype=torch.float32)
     with torch.cuda.device(query.device):
-        rc = spruce_hip.lib().spruce_teacher_block_mass(
+        rc = lib.spruce_teacher_block_mass_schedule(
             spruce_hip.ptr(query), spruce_hip.strides(query), spruce_hip.ptr(key), spruce_hip.strides(key),
             b, H, Hkv, q_len, d, float(scaling), spruce_hip.dtype_code(query),
-            spruce_hip.ptr(mass), spruce_hip.ptr(ws), nbytes, spruce_hip.stream_of(query))
+            spruce_hip.ptr(mass), spruce_hip.ptr(ws), nbytes, code, spruce_hip.stream_of(query))
     spruce_hip.check(rc, "spruce_teacher_block_mass")
     return mass
 
