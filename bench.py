@@ -66,17 +66,43 @@ def _traffic(name):
         return None
 
 
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def _numpy_threads():
+    try:
+        from threadpoolctl import threadpool_info
+        return max((i.get("num_threads") or 0) for i in threadpool_info()) or None
+    except Exception:
+        return None
+
+
+def _cpu_time(fn):
+    """One untimed warm-up call, then the median of three timed calls (s)."""
+    fn()
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
 def cpu_baseline(q, k, v, mask_kv, sample_blocks):
     """Time the float32 numpy oracle on a sample of query blocks of cfg2."""
     import numpy as np
 
     import oracle.attention as ora
-    threads = None
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max((i.get("num_threads") or 0) for i in threadpool_info()) or None
-    except Exception:
-        pass
+    threads = _numpy_threads()
     qn, kn, vn = (x.float().cpu().numpy() for x in (q, k, v))
     mk = mask_kv.cpu().numpy()
     ora.sparse_attention_mask(qn, kn, vn, mk, qblocks_subset=sample_blocks[:1])  # warm-up
@@ -90,11 +116,72 @@ def cpu_baseline(q, k, v, mask_kv, sample_blocks):
         "value": round(flops / dt / 1e12, 6),
         "unit": "TFLOP/s",
         "cores": threads or os.cpu_count(),
+        "cpu_model": _cpu_model(),
         "kind": "port",
         "seconds": round(dt, 3),
         "sample": (f"oracle/attention.py float32 numpy, {len(sample_blocks)} of 512 query blocks "
                    f"x 4 KV heads x 7 query heads of cfg2, {sel * G} head-blocks"),
     }
+
+
+def cpu_baseline_selector(q3, k3, Wq, Wk, top_k, nbytes):
+    """cfg3 on the host: the reference's flat selector restated with float32
+    torch ops (oracle/reference_cpu.py), the whole configuration."""
+    import torch
+
+    import oracle.reference_cpu as rc
+    qc, kc = q3.cpu(), k3.cpu()
+    dt = _cpu_time(lambda: rc.flat_select(qc, kc, Wq, Wk, top_k=top_k))
+    return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "cpu_model": _cpu_model(), "kind": "port", "seconds": round(dt, 3),
+            "sample": "whole cfg3 (group mean, block mean/max, projections, MaxSim, stable top-32), "
+                      "float32 torch, median of 3"}
+
+
+def cpu_baseline_teacher(q4, k4, scale, heads, flop_per_head):
+    """cfg4 on the host: the reference's chunked_pool (float32 torch,
+    oracle/reference_cpu.py) on a slice of query heads, plus the targets of
+    the full mass tensor."""
+    import torch
+
+    import oracle.reference_cpu as rc
+    qc, kc = q4.cpu(), k4.cpu()
+    H = qc.shape[1]
+
+    def run():
+        mass = rc.chunked_pool(qc, kc, scale, heads=heads)
+        rc.teacher_targets(mass, kc.shape[1], k=8)
+
+    dt = _cpu_time(run)
+    return {"value": round(flop_per_head * len(heads) / dt / 1e12, 6), "unit": "TFLOP/s",
+            "cores": torch.get_num_threads(), "cpu_model": _cpu_model(), "kind": "port",
+            "seconds": round(dt, 3),
+            "sample": (f"chunked_pool on {len(heads)} of {H} query heads (all 256 query blocks) + "
+                       "targets, float32 torch, median of 3; TFLOP/s over the sampled heads")}
+
+
+def cpu_baseline_csr(q5, k5, v5, indptr, indices, kv_head, qblocks, G):
+    """cfg5 on the host: the float32 numpy oracle (oracle/attention.py) on one
+    KV head and a sample of its query blocks."""
+    import numpy as np
+
+    import oracle.attention as ora
+    Qb = indptr.numel() // k5.shape[1]
+    qs = q5[:, kv_head * G:(kv_head + 1) * G].float().cpu().numpy()
+    ks = k5[:, kv_head:kv_head + 1].float().cpu().numpy()
+    vs = v5[:, kv_head:kv_head + 1].float().cpu().numpy()
+    ip = indptr[kv_head * Qb:(kv_head + 1) * Qb + 1]
+    ip_n = (ip - ip[0]).numpy()
+    ix_n = indices[int(ip[0]):int(ip[-1])].numpy()
+    t0 = time.perf_counter()
+    ora.sparse_attention_csr(qs, ks, vs, ip_n, ix_n, qblocks_subset=qblocks)
+    dt = time.perf_counter() - t0
+    blocks = sum(int(ip_n[r + 1] - ip_n[r]) for r in qblocks)
+    return {"value": round(blocks * G * BLOCK_FLOPS / dt / 1e12, 6), "unit": "TFLOP/s",
+            "cores": _numpy_threads() or os.cpu_count(), "cpu_model": _cpu_model(), "kind": "port",
+            "seconds": round(dt, 3),
+            "sample": (f"oracle/attention.py float32 numpy, KV head {kv_head} (7 query heads), "
+                       f"{len(qblocks)} of {Qb} query blocks, {blocks} listed key blocks")}
 
 
 def main():
@@ -170,6 +257,9 @@ def main():
             "nnz_kv_blocks": nnz, "flop": flops5,
             "row_blocks_mean": round(float(counts.mean()), 2), "row_blocks_max": int(counts.max()),
         }
+        if not args.no_cpu:
+            configs["cfg5_128k_csr"]["cpu_baseline"] = cpu_baseline_csr(
+                q5, k5, v5, indptr, indices, 0, list(range(0, 2048, 4)), Hq // Hkv)
         # Tree route producer at the cfg5 grid (deployed settings of the
         # reference's export script: radix 2, beam 16, local window 1,
         # k_selected = beam + 2): prototype features of Q and K, the key tree,
@@ -242,6 +332,9 @@ def main():
             "compulsory_bytes": by3, "top_k": 32,
             "stages": "pool (Q group+block mean, K mean/max) -> project -> MaxSim scores -> causal top-k",
         }
+        if not args.no_cpu:
+            configs["cfg3_selector_64k"]["cpu_baseline"] = cpu_baseline_selector(
+                q3, k3, Wq.cpu(), Wk.cpu(), 32, by3)
 
         # Selector prototype features of the reference's capture hook: Q
         # group-averaged and pooled to mean + 7 outliers per block, K likewise.
@@ -311,6 +404,9 @@ def main():
             "flop": fl4, "top_k": 8,
             "note": "algorithmic FLOP = QK^T once over causal blocks (the single-pass kernel computes it once)",
         }
+        if not args.no_cpu:
+            configs["cfg4_teacher_16k"]["cpu_baseline"] = cpu_baseline_teacher(
+                q4, k4, scale, list(range(0, Hq, 4)), fl4 / Hq)
         del q4, k4
 
     if args.calib_copy:
