@@ -4,15 +4,15 @@ TEST INFRASTRUCTURE ONLY.  Nothing in the shipped package imports this file;
 only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it,
 as the checker of the HIP kernels.
 
-Restates the reference's PyTorch oracle, sparse/attention.py:276-364, in
+Restates the reference's PyTorch oracle, sparse/attention.py:186-274, in
 numpy float32:
-  for each query block qb, batch b and KV head g (sparse/attention.py:276-281)
-    ids  = selected[b, g, qb][selected >= 0]            (:282-289; empty -> ValueError)
-    keys = ids * block + arange(block), keeping keys < T (:294-297)
-    s    = (q_blk @ k_sel^T) / sqrt(D) in float32       (:303-309)
-    s[key > query] = finfo.min                          (:313-314)
-    out  = softmax(s) @ v_sel                           (:356-359)
-and returns [B, T, Hq, D] (:364).
+  for each query block qb, batch b and KV head g (sparse/attention.py:186-191)
+    ids  = selected[b, g, qb][selected >= 0]            (:192-199; empty -> ValueError)
+    keys = ids * block + arange(block), keeping keys < T (:204-207)
+    s    = (q_blk @ k_sel^T) / sqrt(D) in float32       (:217-219)
+    s[key > query] = finfo.min                          (:223-224)
+    out  = softmax(s) @ v_sel                           (:266-269)
+and returns [B, T, Hq, D] (:274).
 
 Deliberate, documented choices where the reference has no single answer:
   * block IDs above the query block are dropped.  In the reference oracle such

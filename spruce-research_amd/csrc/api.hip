@@ -114,11 +114,18 @@ extern "C" int spruce_kernel_metadata(int variant, int64_t Hq, int64_t Hkv, int6
   SPRUCE_REQUIRE(json && n, "json buffer required");
   const LaunchShape s = choose_shape(variant, (int)(Hq / Hkv));
   const int lds = 2 * (kBlock * ((int)D + 8) + (int)D * (kBlock + 8)) * 2;
+  // best_config carries the reference's keys (kwargs, num_warps, num_stages,
+  // num_ctas; kernels/seerattention_direct_index_triton.py:419-427) filled
+  // with this launch: waves per workgroup, two K/V stages, one workgroup per
+  // (row, part), the tile constants as kwargs; then the HIP-specific fields.
   const int w = snprintf(json, n,
-                         "{\"variant\":\"%s\",\"best_config\":{\"waves_per_workgroup\":%d,"
+                         "{\"variant\":\"%s\",\"best_config\":{"
+                         "\"kwargs\":{\"QUERY_ROWS\":32,\"KEY_BLOCK\":64,\"TILES_PER_WORKGROUP\":%d,"
+                         "\"WORKGROUPS_PER_ROW\":%d},\"num_warps\":%d,\"num_stages\":2,\"num_ctas\":1,"
+                         "\"waves_per_workgroup\":%d,"
                          "\"workgroups_per_row\":%d,\"query_rows_per_wave\":32,\"key_block\":64,"
                          "\"lds_bytes\":%d,\"mfma\":\"v_mfma_f32_32x32x16\",\"prescale_q\":%s}}",
-                         names[variant], s.waves, s.parts, lds,
+                         names[variant], s.tpp, s.parts, s.waves, s.waves, s.parts, lds,
                          variant == SPRUCE_VARIANT_SINGLE_HEAD_PRESCALE ? "true" : "false");
   return (w < 0 || (size_t)w >= n) ? set_error(SPRUCE_EINVAL, "json buffer too small") : SPRUCE_OK;
 }

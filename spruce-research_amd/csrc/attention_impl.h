@@ -1,6 +1,6 @@
 // Block-sparse causal GQA prefill forward for gfx950.
 //
-// Semantics follow the reference PyTorch path sparse/attention.py:276-364 and
+// Semantics follow the reference PyTorch path sparse/attention.py:186-274 and
 // the kernels it stands in for (kernels/seerattention_direct_index_triton.py:
 // 27-121, kernels/seerattention_triton.py:18-68): for every query token t of
 // query block qb and query head h, softmax(q_t . k_j * scale) over the keys j

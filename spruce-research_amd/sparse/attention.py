@@ -2,7 +2,7 @@
 
 Drop-in for the reference's sparse/attention.py: ``SPARSE_PREFILL_ATTENTION``,
 ``sparse_prefill_attention_forward`` with the same signature, validation
-messages and exception types (sparse/attention.py:119-190, 276-289), and
+messages and exception types (sparse/attention.py:41-81, 83-184, 192-199), and
 ``register_sparse_prefill_attention``.  The reference computes this with a
 host loop of small PyTorch ops; here the whole layer is one launch of the
 gfx950 direct-index kernel, which reads ``selected_blocks[:, layer_idx]`` in
@@ -47,7 +47,7 @@ def _layer_index(module: torch.nn.Module) -> int:
 
 
 def _validate_inputs(query, key, value, selected_blocks, block_size, layer_idx, validate_blocks):
-    """Shape checks of sparse/attention.py:131-170, same messages."""
+    """Shape checks of sparse/attention.py:41-81, same messages."""
     if query.dim() != 4 or key.dim() != 4 or value.dim() != 4:
         raise ValueError("query, key, and value must be [batch, heads, tokens, head_dim]")
     if key.shape != value.shape:
@@ -139,7 +139,7 @@ def sparse_prefill_attention_forward(
     if block_size != 64:
         raise ValueError("the HIP sparse-prefill kernel requires block_size=64")
     indices = selected_blocks[:, layer_idx].to(device=query.device, dtype=torch.int32).contiguous()
-    # The reference raises on a row with no selected block (sparse/attention.py:284-289).
+    # The reference raises on a row with no selected block (sparse/attention.py:192-199).
     empty = ~(indices >= 0).any(dim=-1)
     if bool(empty.any()):
         b, g, qb = (int(x) for x in torch.nonzero(empty)[0])
@@ -166,7 +166,7 @@ def sparse_prefill_attention_forward(
 
 
 def register_sparse_prefill_attention(name: str = SPARSE_PREFILL_ATTENTION) -> str:
-    """Register this backend with Transformers (sparse/attention.py:367-382).
+    """Register this backend with Transformers (sparse/attention.py:277-292).
 
     Prefill receives no O(T^2) mask (the kernel is causal by construction);
     decode keeps SDPA's mask.

@@ -93,3 +93,8 @@ def test_kernel_metadata_reports_launch_shape():
     # Every query head of the KV group is covered: 7 heads x 64 rows per row.
     assert best["waves_per_workgroup"] * best["workgroups_per_row"] * best["query_rows_per_wave"] >= 7 * 64
     assert spruce_hip.launch_config("single_head_prescale", 8, 2, 64)["best_config"]["prescale_q"]
+    # The reference's best_config keys (kernels/seerattention_direct_index_triton.py:419-427),
+    # which its profiling scripts serialise.
+    assert {"kwargs", "num_warps", "num_stages", "num_ctas"} <= set(best)
+    assert isinstance(best["kwargs"], dict) and best["num_warps"] == best["waves_per_workgroup"]
+    assert all(isinstance(best[k], int) for k in ("num_warps", "num_stages", "num_ctas"))
