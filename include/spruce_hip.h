@@ -176,6 +176,29 @@ int spruce_sparse_prefill_index_summaries(
     void* stream);
 
 /*
+ * spruce_sparse_prefill_index (or _summaries when S > 0) for padded batches:
+ * the padded-batch prefill of sparse_prefill_attention_forward
+ * (sparse/attention.py:147-150 reduce the 4-D decoder mask to key validity,
+ * :225-229 add it to the scores).  key_valid uint8 [B, T] (batch stride kvs
+ * elements, tokens contiguous): nonzero marks a real token; a key with
+ * key_valid == 0 gets no weight in any row.  Pass nodes = NULL and S = 0 for
+ * no residual summaries.  A query row whose causal listed keys are all
+ * padding (a left-padded position) writes zeros.
+ */
+int spruce_sparse_prefill_index_masked(
+    const void* q, const int64_t qs[4],
+    const void* k, const int64_t ks[4],
+    const void* v, const int64_t vs[4],
+    const int32_t* idx, const int64_t is[4], int64_t K,
+    const uint8_t* key_valid, int64_t kvs,
+    const int32_t* nodes, const int64_t ns[4], int64_t S,
+    const float* sum_keys, const float* sum_values, const float* sum_log_counts, int64_t N, int64_t P,
+    int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D,
+    float scale, int dtype, int variant,
+    void* out, const int64_t os[4],
+    void* stream);
+
+/*
  * Residual-tree frontiers.  Replaces build_residual_summary_nodes /
  * residual_frontier_for_row (interfaces/residual_summaries.py:119-222): for
  * each row (b, l, g, q) of selected [B, L, G, Qb, K] int32 (element strides

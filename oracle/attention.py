@@ -47,16 +47,19 @@ def _softmax_rows(s):
     return p / p.sum(axis=-1, keepdims=True)
 
 
-def _attend_group(qblk, keys, vals, q_pos, key_idx, scale):
-    """qblk [H, n, D], keys/vals [m, D] -> [H, n, D] (float32)."""
+def _attend_group(qblk, keys, vals, q_pos, key_idx, scale, key_ok=None):
+    """qblk [H, n, D], keys/vals [m, D] -> [H, n, D] (float32).  key_ok [m]:
+    key padding, scored finfo.min like the causal fill."""
     s = np.matmul(qblk, keys.T) * np.float32(scale) if scale is not None else \
         np.matmul(qblk, keys.T) / np.float32(math.sqrt(qblk.shape[-1]))
     causal = key_idx[None, :] <= q_pos[:, None]
+    if key_ok is not None:
+        causal = causal & key_ok[None, :]
     s = np.where(causal[None], s, F32_MIN)
     return np.matmul(_softmax_rows(s), vals).astype(np.float32)
 
 
-def _sparse_attention(q, k, v, blocks_for, block_size, scale, empty, qblocks_subset=None):
+def _sparse_attention(q, k, v, blocks_for, block_size, scale, empty, qblocks_subset=None, key_valid=None):
     q = np.asarray(q, dtype=np.float32)
     k = np.asarray(k, dtype=np.float32)
     v = np.asarray(v, dtype=np.float32)
@@ -89,18 +92,25 @@ def _sparse_attention(q, k, v, blocks_for, block_size, scale, empty, qblocks_sub
                             f"batch={b}, kv_head={g}, query_block={qb}")
                     key_idx = (ids[:, None] * block_size + offs[None, :]).reshape(-1)
                     key_idx = key_idx[key_idx < T]
+                    key_ok = None if key_valid is None else np.asarray(key_valid[b], dtype=bool)[key_idx]
                     out[b, heads, q0:q1] = _attend_group(
                         q[b, heads, q0:q1], k[b, g, key_idx], v[b, g, key_idx],
-                        q_pos, key_idx, scale)
+                        q_pos, key_idx, scale, key_ok)
     return out.transpose(0, 2, 1, 3).copy()
 
 
 def sparse_attention_index(q, k, v, idx, block_size=64, scale=None, empty="raise",
-                           qblocks_subset=None):
-    """Padded direct-index lists ``idx [B, Hkv, Qb, K]`` -> ``[B, T, Hq, D]``."""
+                           qblocks_subset=None, key_valid=None):
+    """Padded direct-index lists ``idx [B, Hkv, Qb, K]`` -> ``[B, T, Hq, D]``.
+
+    key_valid: optional bool ``[B, T]`` key padding; padding keys get the
+    finfo.min score of the reference's additive decoder mask
+    (sparse/attention.py:225-229).  Rows at padding query positions whose
+    listed causal keys are all padding are then a uniform average (the
+    reference's result too); callers compare real positions only."""
     idx = np.asarray(idx)
     return _sparse_attention(q, k, v, lambda b, g, qb: idx[b, g, qb], block_size, scale, empty,
-                             qblocks_subset)
+                             qblocks_subset, key_valid)
 
 
 def sparse_attention_csr(q, k, v, indptr, indices, block_size=64, scale=None, empty="raise",
@@ -187,10 +197,12 @@ def attention_bruteforce(q, k, v, key_sets, scale=None):
 
 
 def sparse_attention_summaries(q, k, v, idx, nodes, sum_keys, sum_values, sum_log_counts,
-                               block_size=64, scale=None, qblocks_subset=None):
+                               block_size=64, scale=None, qblocks_subset=None, key_valid=None):
     """Padded lists ``idx [B,Hkv,Qb,K]`` plus summary rows ``nodes [B,Hkv,Qb,S]``
     over a table ``sum_keys/sum_values [B,Hkv,N,P,D]``, ``sum_log_counts
-    [B,N,P]`` (natural log, -inf for empty prototypes) -> ``[B,T,Hq,D]``."""
+    [B,N,P]`` (natural log, -inf for empty prototypes) -> ``[B,T,Hq,D]``.
+    key_valid: optional bool ``[B, T]`` key padding of the exact keys (the
+    table is then built over the real tokens only)."""
     q = np.asarray(q, dtype=np.float32)
     k = np.asarray(k, dtype=np.float32)
     v = np.asarray(v, dtype=np.float32)
@@ -224,7 +236,10 @@ def sparse_attention_summaries(q, k, v, idx, nodes, sum_keys, sum_values, sum_lo
                 heads = slice(g * G, (g + 1) * G)
                 qh = q[b, heads, q0:q1]
                 s = scaled(np.matmul(qh, k[b, g, key_idx].T))
-                s = np.where((key_idx[None, :] <= q_pos[:, None])[None], s, F32_MIN)
+                ok = key_idx[None, :] <= q_pos[:, None]
+                if key_valid is not None:
+                    ok = ok & np.asarray(key_valid[b], dtype=bool)[key_idx][None, :]
+                s = np.where(ok[None], s, F32_MIN)
                 vals = v[b, g, key_idx]
                 row = np.asarray(nodes[b, g, qb], dtype=np.int64)
                 row = row[(row >= 0) & (row < N)]

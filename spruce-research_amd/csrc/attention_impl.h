@@ -72,6 +72,10 @@ struct AttnParams {
   const uint8_t* mask;
   int64_t ms[4];
   int mask_per_qhead;
+  // key padding (padded-list form only): kvalid[b * kvs + t] != 0 marks a
+  // real key token; padding keys get no weight.
+  const uint8_t* kvalid;
+  int64_t kvs;
   // residual summaries (sparse/attention.py:226-265): per row, nodes
   // [B, Hkv, Qb, S] int32 (-1 = none); table keys/values float32
   // [B, Hkv, N, P, D] and natural-log counts [B, N, P], all contiguous.
@@ -474,10 +478,12 @@ constexpr int kSchedDsRead = 0x100;
 // K k-steps (two reads each; the V^T loop keeps the same number of reads).
 constexpr int kLookahead = 2;
 
-template <int D, int WAVES, typename TIn, bool F16, int MODE, bool SUMM = false, bool CAP = false, bool PROD = false>
+template <int D, int WAVES, typename TIn, bool F16, int MODE, bool SUMM = false, bool CAP = false, bool PROD = false,
+          bool KVAL = false>
 __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnParams p) {
   static_assert(!CAP || (MODE == kModeCausal && !SUMM && TIn::bytes == 2),
                 "feature capture runs on the dense causal form in the model dtype");
+  static_assert(!KVAL || MODE == kModePadded, "key padding is supported for padded block lists");
   static_assert(!PROD || (!SUMM && TIn::bytes == 2), "the producer form stages 16-bit K/V for key blocks only");
   constexpr int NTHR = WAVES * 64;
   constexpr int KSTR = D + 8;        // K tile row stride, 16-bit elements (16 B pad)
@@ -727,8 +733,18 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     sc1 = s1;
   };
   // sb: per-key score bias of a summary chunk (null for a key block).
-  auto softmax = [&](bool diag, const float* sb) {
+  // vb: validity bits of the block's 64 keys (key padding; all set otherwise).
+  auto softmax = [&](bool diag, const float* sb, uint64_t vb) {
     f32x16_t s0 = sc0, s1 = sc1;
+    if constexpr (KVAL) {
+      // Register r of key tile c holds key 32c + 8(r/4) + 4(lane/32) + r%4.
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kr = 8 * (r >> 2) + 4 * hl + (r & 3);
+        if (!((vb >> kr) & 1ull)) s0[r] = -INFINITY;
+        if (!((vb >> (32 + kr)) & 1ull)) s1[r] = -INFINITY;
+      }
+    }
     if (diag) {
       // Register r of key tile c holds key 32c + 8(r/4) + 4(lane/32) + r%4.
       const int thr = qin - 4 * hl;
@@ -760,7 +776,9 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     const float cand = mx * p.cs;
     if (__ballot(cand > m_use + kRescaleThreshold) != 0) {
       const float m_new = fmaxf(m_use, cand);
-      const float alpha = fast_exp2(m_use - m_new);
+      // With key padding a padded query row can still have no usable key
+      // while others in the wave do: keep its (empty) state as it is.
+      const float alpha = (KVAL && m_new == -INFINITY) ? 1.f : fast_exp2(m_use - m_new);
       m_use = m_new;
       l_run *= alpha;
 #pragma unroll
@@ -770,7 +788,7 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     }
     // A lane whose keys so far are all -inf (a summary-only row) keeps
     // m_use = -inf; exp2(-inf) = 0 needs a finite offset there.
-    const float nm = (sb != nullptr && m_use == -INFINITY) ? 0.f : -m_use;
+    const float nm = ((KVAL || sb != nullptr) && m_use == -INFINITY) ? 0.f : -m_use;
     float psum = 0.f;
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2) {
@@ -814,12 +832,23 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
       acc[dt] = mfma32x32x16<F16>(va[i], pk[c][h2], acc[dt]);
     }
   };
-  auto compute = [&](int buf, bool diag, const float* sb) {
+  auto compute = [&](int buf, bool diag, const float* sb, uint64_t vb) {
     const uint16_t* Ks = smem + buf * BUF;
     scores(Ks);
-    softmax(diag, sb);
+    softmax(diag, sb, vb);
     pv(Ks + KTILE);
   };
+  // Key padding: this lane's validity byte of block `blk` (loaded one block
+  // ahead; the ballot over the wave gives the block's 64 bits).
+  auto vbyte = [&](int blk) -> uint32_t {
+    if constexpr (KVAL) {
+      const int key = blk * kBlock + lane;
+      return key < p.T ? (uint32_t)p.kvalid[(int64_t)b * p.kvs + key] : 0u;
+    } else {
+      return 1u;
+    }
+  };
+  auto vbits = [&](uint32_t raw) -> uint64_t { return KVAL ? __ballot(raw != 0u) : ~0ull; };
 
   BlockIter<MODE> it;
   it.init(p, b, g, qb, part, hq, lane, half_major);
@@ -843,20 +872,24 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
         }
       } else {
         if (!q_ready) convert_q();
+        uint32_t vcur = vbyte(cur_id);
         __syncthreads();
         while (true) {
           int nid = 0;
           bool nen = false;
           const bool more = it.next(nid, nen);
-          if (active && cur_en) compute(buf, cur_id == qb, nullptr);
+          const uint32_t vnext = more ? vbyte(nid) : 0u;
+          if (active && cur_en) compute(buf, cur_id == qb, nullptr, vbits(vcur));
           if (!more) break;
           __syncthreads();
           buf ^= 1;
           cur_id = nid;
           cur_en = nen;
+          vcur = vnext;
         }
       }
     } else {
+      uint32_t vcur = vbyte(cur_id);
       load_block(cur_id);
       if (!q_ready) convert_q();
       store_block(0);
@@ -865,14 +898,16 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
         int nid = 0;
         bool nen = false;
         const bool more = it.next(nid, nen);
+        const uint32_t vnext = more ? vbyte(nid) : 0u;
         if (more) load_block(nid);
-        if (active && cur_en) compute(buf, cur_id == qb, nullptr);
+        if (active && cur_en) compute(buf, cur_id == qb, nullptr, vbits(vcur));
         if (!more) break;
         store_block(buf ^ 1);
         __syncthreads();
         buf ^= 1;
         cur_id = nid;
         cur_en = nen;
+        vcur = vnext;
       }
     }
   }
@@ -931,7 +966,7 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
         sbias[buf][tid] = node < 0 ? -INFINITY : p.slog[((int64_t)b * p.N + node) * p.P + en % p.P] * p.sbias;
       }
       __syncthreads();
-      if (active) compute(buf, false, sbias[buf]);
+      if (active) compute(buf, false, sbias[buf], ~0ull);
     }
   }
 
@@ -1057,40 +1092,41 @@ inline LaunchShape choose_shape(int variant, int G) {
   return tiles % 4 == 0 ? LaunchShape{4, tiles / 4, 4} : LaunchShape{2, tiles / 2, 2};
 }
 
-template <int D, int WAVES, typename TIn, bool F16, int MODE, bool SUMM, bool CAP = false, bool PROD = false>
+template <int D, int WAVES, typename TIn, bool F16, int MODE, bool SUMM, bool CAP = false, bool PROD = false,
+          bool KVAL = false>
 int launch_attention_t(const AttnParams& p, hipStream_t stream) {
   // Rows are padded to a multiple of the 8 XCDs; the extra workgroups exit.
   const int64_t rows8 = ((int64_t)p.B * p.Hkv * p.Qb + 7) / 8 * 8;
   const int64_t grid = rows8 * p.parts;
-  hipLaunchKernelGGL((sparse_prefill_kernel<D, WAVES, TIn, F16, MODE, SUMM, CAP, PROD>), dim3((unsigned)grid),
+  hipLaunchKernelGGL((sparse_prefill_kernel<D, WAVES, TIn, F16, MODE, SUMM, CAP, PROD, KVAL>), dim3((unsigned)grid),
                      dim3(WAVES * 64), 0, stream, p);
   return check_launch("sparse_prefill_kernel");
 }
 
-template <int MODE, bool SUMM, int D, typename TIn, bool F16>
+template <int MODE, bool SUMM, int D, typename TIn, bool F16, bool KVAL>
 int launch_attention_w(const AttnParams& p, int waves, hipStream_t stream) {
   switch (waves) {
-    case 2: return launch_attention_t<D, 2, TIn, F16, MODE, SUMM>(p, stream);
-    case 4: return launch_attention_t<D, 4, TIn, F16, MODE, SUMM>(p, stream);
+    case 2: return launch_attention_t<D, 2, TIn, F16, MODE, SUMM, false, false, KVAL>(p, stream);
+    case 4: return launch_attention_t<D, 4, TIn, F16, MODE, SUMM, false, false, KVAL>(p, stream);
     case 8:
       // A spare wave becomes the K/V producer (16-bit inputs, key blocks only).
       if constexpr (kUseProducer && TIn::bytes == 2 && !SUMM)
-        if (p.tpp < 8) return launch_attention_t<D, 8, TIn, F16, MODE, SUMM, false, true>(p, stream);
-      return launch_attention_t<D, 8, TIn, F16, MODE, SUMM>(p, stream);
+        if (p.tpp < 8) return launch_attention_t<D, 8, TIn, F16, MODE, SUMM, false, true, KVAL>(p, stream);
+      return launch_attention_t<D, 8, TIn, F16, MODE, SUMM, false, false, KVAL>(p, stream);
     default: return set_error(SPRUCE_EINVAL, "unsupported wave count %d", waves);
   }
 }
 
-template <int MODE, bool SUMM = false>
+template <int MODE, bool SUMM = false, bool KVAL = false>
 int launch_attention(const AttnParams& p, int D, int dtype, int waves, hipStream_t stream) {
   if (D == 128) {
-    if (dtype == SPRUCE_DTYPE_BF16) return launch_attention_w<MODE, SUMM, 128, InBF16, false>(p, waves, stream);
-    if (dtype == SPRUCE_DTYPE_F16) return launch_attention_w<MODE, SUMM, 128, InF16, true>(p, waves, stream);
-    return launch_attention_w<MODE, SUMM, 128, InF32, false>(p, waves, stream);
+    if (dtype == SPRUCE_DTYPE_BF16) return launch_attention_w<MODE, SUMM, 128, InBF16, false, KVAL>(p, waves, stream);
+    if (dtype == SPRUCE_DTYPE_F16) return launch_attention_w<MODE, SUMM, 128, InF16, true, KVAL>(p, waves, stream);
+    return launch_attention_w<MODE, SUMM, 128, InF32, false, KVAL>(p, waves, stream);
   }
-  if (dtype == SPRUCE_DTYPE_BF16) return launch_attention_w<MODE, SUMM, 64, InBF16, false>(p, waves, stream);
-  if (dtype == SPRUCE_DTYPE_F16) return launch_attention_w<MODE, SUMM, 64, InF16, true>(p, waves, stream);
-  return launch_attention_w<MODE, SUMM, 64, InF32, false>(p, waves, stream);
+  if (dtype == SPRUCE_DTYPE_BF16) return launch_attention_w<MODE, SUMM, 64, InBF16, false, KVAL>(p, waves, stream);
+  if (dtype == SPRUCE_DTYPE_F16) return launch_attention_w<MODE, SUMM, 64, InF16, true, KVAL>(p, waves, stream);
+  return launch_attention_w<MODE, SUMM, 64, InF32, false, KVAL>(p, waves, stream);
 }
 
 // Shared argument checks and parameter setup of the three entry points.

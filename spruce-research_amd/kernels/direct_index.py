@@ -53,11 +53,22 @@ def _record(kernel_variant, Hq, Hkv, D):
         kernel_variant, Hq, Hkv, D)["best_config"]
 
 
+def _key_valid(key_valid, B, T, device):
+    """bool/uint8 ``[B, T]`` key validity -> contiguous uint8 on ``device``."""
+    if key_valid.shape != (B, T):
+        raise ValueError(f"key_valid must be [B, T] = {(B, T)}, got {tuple(key_valid.shape)}")
+    if key_valid.device != device:
+        raise ValueError("key_valid must be on the same device as q")
+    return key_valid.to(torch.bool).contiguous().view(torch.uint8)
+
+
 def direct_index_sparse_prefill(q, k, v, indices, scale, block_size=64,
-                                kernel_variant="single_head"):
+                                kernel_variant="single_head", key_valid=None):
     """Causal block-sparse attention over exactly the supplied block IDs.
 
     indices: int32 ``[B,Hkv,ceil(T/64),K]``; negative entries are padding.
+    key_valid: optional bool ``[B,T]`` key padding (False keys get no weight;
+    a query row with no valid causal listed key writes zeros).
     Returns ``[B,T,Hq,D]`` in q's dtype.
     """
     B, Hq, Hkv, T, D = _check_common(q, k, v, block_size, kernel_variant)
@@ -71,6 +82,22 @@ def direct_index_sparse_prefill(q, k, v, indices, scale, block_size=64,
     if indices.device != q.device:
         raise ValueError("indices must be on the same device as q")
     out, out_strides = _output(q)
+    if key_valid is not None:
+        kv8 = _key_valid(key_valid, B, T, q.device)
+        zero4 = spruce_hip.strides(torch.empty(0, 0, 0, 0))
+        with torch.cuda.device(q.device):
+            rc = spruce_hip.lib().spruce_sparse_prefill_index_masked(
+                spruce_hip.ptr(q), spruce_hip.strides(q),
+                spruce_hip.ptr(k), spruce_hip.strides(k),
+                spruce_hip.ptr(v), spruce_hip.strides(v),
+                spruce_hip.ptr(indices), spruce_hip.strides(indices), indices.shape[3],
+                spruce_hip.ptr(kv8), T, None, zero4, 0, None, None, None, 0, 1,
+                B, Hq, Hkv, T, D, float(scale), spruce_hip.dtype_code(q),
+                spruce_hip.variant_code(kernel_variant),
+                spruce_hip.ptr(out), out_strides, spruce_hip.stream_of(q))
+        spruce_hip.check(rc, "spruce_sparse_prefill_index_masked")
+        _record(kernel_variant, Hq, Hkv, D)
+        return out
     with torch.cuda.device(q.device):
         rc = spruce_hip.lib().spruce_sparse_prefill_index(
             spruce_hip.ptr(q), spruce_hip.strides(q),
@@ -86,7 +113,7 @@ def direct_index_sparse_prefill(q, k, v, indices, scale, block_size=64,
 
 
 def direct_index_sparse_summaries(q, k, v, indices, nodes, table, scale, block_size=64,
-                                  kernel_variant="single_head"):
+                                  kernel_variant="single_head", key_valid=None):
     """Direct-index attention plus residual summaries (sparse/attention.py:226-265).
 
     indices: int32 ``[B,Hkv,ceil(T/64),K]``; nodes: int32 ``[B,Hkv,ceil(T/64),S]``
@@ -94,7 +121,9 @@ def direct_index_sparse_summaries(q, k, v, indices, nodes, table, scale, block_s
     ``sparse.summaries.build_kv_summary_table`` over the same K/V (keys/values
     ``[B,Hkv,N,P,D]`` float32, log_counts ``[B,N,P]``).  Every listed node adds
     one softmax entry per prototype with a non-empty slice: the summary key's
-    score plus log(count), and the summary value.  Returns ``[B,T,Hq,D]``.
+    score plus log(count), and the summary value.  key_valid: optional bool
+    ``[B,T]`` key padding for the exact keys (the table should be built with
+    the same token mask).  Returns ``[B,T,Hq,D]``.
     """
     B, Hq, Hkv, T, D = _check_common(q, k, v, block_size, kernel_variant)
     qblocks = (T + block_size - 1) // block_size
@@ -114,6 +143,24 @@ def direct_index_sparse_summaries(q, k, v, indices, nodes, table, scale, block_s
     if any(t.device != q.device for t in (indices, nodes, keys, values, logc)):
         raise ValueError("indices, nodes and the summary table must be on the same device as q")
     out, out_strides = _output(q)
+    if key_valid is not None:
+        kv8 = _key_valid(key_valid, B, T, q.device)
+        with torch.cuda.device(q.device):
+            rc = spruce_hip.lib().spruce_sparse_prefill_index_masked(
+                spruce_hip.ptr(q), spruce_hip.strides(q),
+                spruce_hip.ptr(k), spruce_hip.strides(k),
+                spruce_hip.ptr(v), spruce_hip.strides(v),
+                spruce_hip.ptr(indices), spruce_hip.strides(indices), indices.shape[3],
+                spruce_hip.ptr(kv8), T,
+                spruce_hip.ptr(nodes), spruce_hip.strides(nodes), nodes.shape[3],
+                spruce_hip.ptr(keys), spruce_hip.ptr(values), spruce_hip.ptr(logc),
+                keys.shape[2], keys.shape[3],
+                B, Hq, Hkv, T, D, float(scale), spruce_hip.dtype_code(q),
+                spruce_hip.variant_code(kernel_variant),
+                spruce_hip.ptr(out), out_strides, spruce_hip.stream_of(q))
+        spruce_hip.check(rc, "spruce_sparse_prefill_index_masked")
+        _record(kernel_variant, Hq, Hkv, D)
+        return out
     with torch.cuda.device(q.device):
         rc = spruce_hip.lib().spruce_sparse_prefill_index_summaries(
             spruce_hip.ptr(q), spruce_hip.strides(q),

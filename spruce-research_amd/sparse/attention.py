@@ -14,10 +14,18 @@ summary table of the layer's K/V is built on the GPU
 (``build_kv_summary_table``) and the same kernel appends one key per listed
 node and non-empty prototype, scored q.k/sqrt(D) + log(count).
 
+Padded batches (sparse/attention.py:147-150, 173-176, 225-229): a 4-D
+decoder mask -- boolean (True attends, Transformers' sdpa_mask) or additive
+(0 attends, -inf / finfo.min masks) -- is reduced to per-token key validity,
+which the kernel applies to every listed key block and which the residual
+summary table excludes.  The kernel applies causality itself, so the mask
+must be exactly "causal and key is a real token" at every real query
+position; any other pattern raises.  Outputs at padding query positions are
+not defined (a position with no real causal key writes zeros).
+
 Differences, all raising instead of computing something else:
   * ``block_size`` must be 64 and ``head_dim`` 64 or 128 (the kernel's tile);
-  * ``attention_mask`` must be None (B=1 unpadded prefill; causality is
-    applied by the kernel), as in the reference's kernel backend.
+  * attention masks other than causal key padding (see above).
 """
 import math
 from typing import Optional
@@ -81,6 +89,47 @@ def _validate_inputs(query, key, value, selected_blocks, block_size, layer_idx, 
             f"for seq_len={query.shape[-2]} and block_size={block_size}")
 
 
+def _key_validity(attention_mask: torch.Tensor, batch: int, seq_len: int) -> torch.Tensor:
+    """The 4-D decoder mask as key validity ``[batch, seq_len]`` bool, after
+    checking that the mask is causal key padding at every real query position.
+
+    A key is real when the last query position attends it: in a causal
+    decoder mask that row sees every real key, with left or right padding,
+    and it is never a fully masked padding row that a mask builder may have
+    opened up to keep SDPA from producing NaN."""
+    if attention_mask.dim() != 4:
+        raise ValueError(
+            "Sparse prefill expects the Transformers 4D additive attention mask; "
+            f"got shape {tuple(attention_mask.shape)}")
+    if attention_mask.shape[0] != batch or tuple(attention_mask.shape[-2:]) != (seq_len, seq_len):
+        raise ValueError(
+            f"attention mask {tuple(attention_mask.shape)} does not match batch {batch} and "
+            f"{seq_len} query/key tokens")
+    m = attention_mask
+    if m.shape[1] != 1 and not bool((m == m[:, :1]).all()):
+        raise ValueError("per-head attention masks are not supported by the HIP sparse-prefill path")
+    m = m[:, 0]
+    if m.dtype == torch.bool:
+        attend = m
+    else:
+        attend = m >= 0
+        if bool((m[attend] != 0).any()) or bool((m[~attend] > torch.finfo(m.dtype).min / 2).any()):
+            raise ValueError(
+                "additive attention masks must hold 0 (attend) or -inf / finfo.min (masked); "
+                "score biases are not supported by the HIP sparse-prefill path")
+    valid = attend[:, -1, :]
+    keys = torch.arange(seq_len, device=m.device)
+    for r0 in range(0, seq_len, 2048):
+        r1 = min(r0 + 2048, seq_len)
+        expected = (keys[None, :] <= keys[r0:r1, None])[None] & valid[:, None, :]
+        wrong = (attend[:, r0:r1] != expected) & valid[:, r0:r1, None]
+        if bool(wrong.any()):
+            raise ValueError(
+                "the HIP sparse-prefill path applies causal attention with key padding only; "
+                "this attention mask has another pattern")
+    return valid
+
+
 def sparse_prefill_attention_forward(
     module: torch.nn.Module,
     query: torch.Tensor,
@@ -128,14 +177,11 @@ def sparse_prefill_attention_forward(
             validate_residual_summary_nodes(
                 selected_blocks, residual_summary_nodes,
                 validate_selected=not validate_selected_blocks_input)
+    key_valid = None
     if attention_mask is not None:
-        if attention_mask.dim() != 4:
-            raise ValueError(
-                "Sparse prefill expects the Transformers 4D additive attention mask; "
-                f"got shape {tuple(attention_mask.shape)}")
-        raise ValueError(
-            "the HIP sparse-prefill path applies causality itself and supports "
-            "attention_mask=None only (unpadded prefill)")
+        key_valid = _key_validity(attention_mask, query.shape[0], query.shape[-2])
+        if bool(key_valid.all()):
+            key_valid = None      # no padding: the plain kernel
     if block_size != 64:
         raise ValueError("the HIP sparse-prefill kernel requires block_size=64")
     indices = selected_blocks[:, layer_idx].to(device=query.device, dtype=torch.int32).contiguous()
@@ -149,7 +195,8 @@ def sparse_prefill_attention_forward(
     D = query.shape[-1]
     if not residual_summaries:
         output = direct_index_sparse_prefill(
-            query, key, value, indices, scale=1.0 / math.sqrt(D), block_size=block_size)
+            query, key, value, indices, scale=1.0 / math.sqrt(D), block_size=block_size,
+            key_valid=key_valid)
         return output, None
     # Residual summaries (sparse/attention.py:163-182): the frontier nodes of
     # this layer, and the summary table of this layer's K/V over the tree.
@@ -159,23 +206,25 @@ def sparse_prefill_attention_forward(
     nodes = residual_summary_nodes[:, layer_idx].to(device=query.device, dtype=torch.int32).contiguous()
     layout = build_residual_tree_layout(indices.shape[2])
     table = build_kv_summary_table(key, value, layout, block_size=block_size,
-                                   prototypes=summary_prototypes)
+                                   prototypes=summary_prototypes, token_mask=key_valid)
     output = direct_index_sparse_summaries(
-        query, key, value, indices, nodes, table, scale=1.0 / math.sqrt(D), block_size=block_size)
+        query, key, value, indices, nodes, table, scale=1.0 / math.sqrt(D), block_size=block_size,
+        key_valid=key_valid)
     return output, None
 
 
 def register_sparse_prefill_attention(name: str = SPARSE_PREFILL_ATTENTION) -> str:
     """Register this backend with Transformers (sparse/attention.py:277-292).
 
-    Prefill receives no O(T^2) mask (the kernel is causal by construction);
-    decode keeps SDPA's mask.
+    The mask formatter is Transformers' sdpa_mask, as in the reference: no
+    mask for unpadded causal prefill, a boolean [B, 1, T, T] mask for padded
+    batches (reduced to key validity here).
     """
     try:
         from transformers import AttentionInterface, AttentionMaskInterface
+        from transformers.masking_utils import sdpa_mask
     except ImportError as error:
         raise RuntimeError("register_sparse_prefill_attention requires transformers") from error
-    from kernels.sparse_prefill import _triton_attention_mask
     AttentionInterface.register(name, sparse_prefill_attention_forward)
-    AttentionMaskInterface.register(name, _triton_attention_mask)
+    AttentionMaskInterface.register(name, sdpa_mask)
     return name

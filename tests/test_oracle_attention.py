@@ -178,3 +178,39 @@ def test_layouts_agree_and_row_order_is_irrelevant():
     by_mask = sparse_attention_mask(q, k, v, mask, block_size=bs)
     np.testing.assert_allclose(by_csr, by_index, atol=1e-6)
     np.testing.assert_allclose(by_mask, by_index, atol=1e-6)
+
+
+def test_key_padding_matches_bruteforce_at_real_positions():
+    # Padded batches (sparse/attention.py:225-229 in the reference): padding
+    # keys get no weight.  Row 0 right-padded (real tokens 0..4), row 1
+    # left-padded (real tokens 3..8); only real query positions are defined.
+    rng = np.random.default_rng(5)
+    B, Hq, Hkv, T, D, bs = 2, 4, 2, 9, 3, 2
+    qblocks = 5
+    q = rng.standard_normal((B, Hq, T, D)).astype(np.float32)
+    k = rng.standard_normal((B, Hkv, T, D)).astype(np.float32)
+    v = rng.standard_normal((B, Hkv, T, D)).astype(np.float32)
+    valid = np.zeros((B, T), bool)
+    valid[0, :5] = True
+    valid[1, 3:] = True
+    idx = np.full((B, Hkv, qblocks, 3), -1, np.int32)
+    for b in range(B):
+        for g in range(Hkv):
+            for qb in range(qblocks):
+                row = sorted({0, qb, int(rng.integers(0, qb + 1))})
+                idx[b, g, qb, :len(row)] = row
+    out = sparse_attention_index(q, k, v, idx, block_size=bs, key_valid=valid)
+    listed = _bruteforce_keys(lambda b, h, qb: idx[b, h // 2, qb], bs, T)
+    def real_keys(b, h, t):   # padding query positions with no real key are not compared
+        keys = [j for j in listed(b, h, t) if valid[b, j]]
+        return keys or listed(b, h, t)
+
+    ref = np.array(attention_bruteforce(q, k, v, real_keys))
+    for b in range(B):
+        for t in range(T):
+            if valid[b, t]:
+                np.testing.assert_allclose(out[b, t], ref[b, t], atol=1e-5, rtol=1e-5)
+    # All keys valid == no key padding.
+    np.testing.assert_array_equal(
+        sparse_attention_index(q, k, v, idx, block_size=bs, key_valid=np.ones((B, T), bool)),
+        sparse_attention_index(q, k, v, idx, block_size=bs))

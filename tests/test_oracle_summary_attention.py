@@ -44,10 +44,10 @@ def _frontier(sel):
     return out
 
 
-def _table(k, v, qblocks, block_size, P):
+def _table(k, v, qblocks, block_size, P, valid=None):
     lay = osum.tree_layout(qblocks)
     rs, re = osum.token_ranges(lay["starts"], lay["ends"], k.shape[2], block_size, P)
-    keys, vals, _, logc = osum.kv_summary(k, v, rs, re)
+    keys, vals, _, logc = osum.kv_summary(k, v, rs, re, valid)
     N = len(lay["starts"])
     B, H, _, D = k.shape
     return (keys.reshape(B, H, N, P, D), vals.reshape(B, H, N, P, D), logc.reshape(B, N, P))
@@ -87,7 +87,7 @@ def test_reference_kat_all_blocks_have_empty_frontier():
     np.testing.assert_array_equal(out, sparse_attention_index(query, key, value, sel, block_size=2))
 
 
-def _bruteforce(q, k, v, sel, nodes, table_keys, table_vals, table_logc, block_size):
+def _bruteforce(q, k, v, sel, nodes, table_keys, table_vals, table_logc, block_size, valid=None):
     q, k, v = (np.asarray(x, np.float64).tolist() for x in (q, k, v))
     B, Hq, T, D = len(q), len(q[0]), len(q[0][0]), len(q[0][0][0])
     G = Hq // len(k[0])
@@ -102,7 +102,7 @@ def _bruteforce(q, k, v, sel, nodes, table_keys, table_vals, table_logc, block_s
                 for blk in sel[b, g, qb]:
                     if 0 <= blk <= qb:
                         for j in range(blk * block_size, min((blk + 1) * block_size, T)):
-                            if j <= t:
+                            if j <= t and (valid is None or valid[b, j]):
                                 entries.append((k[b][g][j], v[b][g][j], 0.0))
                 for node in nodes[b, g, qb]:
                     if node < 0:
@@ -113,6 +113,8 @@ def _bruteforce(q, k, v, sel, nodes, table_keys, table_vals, table_logc, block_s
                             continue
                         entries.append((table_keys[b, g, node, p].tolist(),
                                         table_vals[b, g, node, p].tolist(), bias))
+                if not entries:   # a padding position with nothing to attend
+                    continue
                 scores = [sum(q[b][h][t][d] * kk[d] for d in range(D)) * sc + bias
                           for kk, _, bias in entries]
                 mx = max(scores)
@@ -143,3 +145,33 @@ def test_bruteforce_random_gqa_ragged(prototypes):
     out = sparse_attention_summaries(q, k, v, sel, nodes, sk, sv, sl, block_size=bs)
     ref = _bruteforce(q, k, v, sel, nodes, sk, sv, sl, bs)
     np.testing.assert_allclose(out, ref, atol=2e-5, rtol=1e-4)
+
+
+def test_bruteforce_with_key_padding():
+    # Padded batches: row 0 right-padded, row 1 left-padded; padding keys get
+    # no weight and the summary table covers the real tokens only.  Real
+    # query positions with at least one entry are compared.
+    rng = np.random.default_rng(7)
+    B, Hq, Hkv, T, D, bs, P = 2, 4, 2, 23, 4, 3, 2
+    Q = (T + bs - 1) // bs
+    q = rng.standard_normal((B, Hq, T, D)).astype(np.float32)
+    k = rng.standard_normal((B, Hkv, T, D)).astype(np.float32)
+    v = rng.standard_normal((B, Hkv, T, D)).astype(np.float32)
+    valid = np.zeros((B, T), bool)
+    valid[0, :15] = True
+    valid[1, 5:] = True
+    sel = np.full((B, Hkv, Q, 5), -1, np.int32)
+    for b, g, qb in np.ndindex(B, Hkv, Q):
+        extra = rng.choice(qb + 1, size=min(qb + 1, 2), replace=False).tolist()
+        row = sorted(set(extra) | {qb, max(0, qb - 1)})
+        sel[b, g, qb, : len(row)] = row
+    nodes = _frontier(sel)
+    sk, sv, sl = _table(k, v, Q, bs, P, valid)
+    out = sparse_attention_summaries(q, k, v, sel, nodes, sk, sv, sl, block_size=bs, key_valid=valid)
+    ref = _bruteforce(q, k, v, sel, nodes, sk, sv, sl, bs, valid)
+    for b in range(B):
+        for t in range(T):
+            if valid[b, t]:
+                np.testing.assert_allclose(out[b, t], ref[b, t], atol=2e-5, rtol=1e-4)
+    unpadded = sparse_attention_summaries(q, k, v, sel, nodes, *_table(k, v, Q, bs, P), block_size=bs)
+    assert np.abs(unpadded[1, 5:] - out[1, 5:]).max() > 1e-2   # the padding changes real rows
