@@ -247,9 +247,20 @@ int spruce_gate_project(const float* x, const float* w, int64_t N, int64_t D, in
                         void* stream);
 
 /*
+ * Two projections in one launch: outa = xa @ wa [Na, P], outb = xb @ wb
+ * [Nb, P], both with the D x P shape and the arithmetic of
+ * spruce_gate_project (identical results).  Replaces the pair
+ * FlatGate.project_queries + project_keys of one layer (selector/gate.py:120-127).
+ */
+int spruce_gate_project2(const float* xa, const float* wa, int64_t Na, const float* xb, const float* wb,
+                         int64_t Nb, int64_t D, int64_t P, float* outa, float* outb, void* stream);
+
+/*
  * MaxSim block scores: scores[s][i][j] = max over prototype pairs (a, c) of
- * qp[s][i][a] . kp[s][j][c], divided by div (= sqrt(P)).  With causal != 0
- * only j <= i is computed and j > i is written as -inf.
+ * qp[s][i][a] . kp[s][j][c], divided by div (= sqrt(P)).  causal = 1: only
+ * j <= i is computed and j > i is written as -inf; causal = 2 with Qb == Kb:
+ * only j <= i is computed and the entries j > i are unspecified (for a
+ * consumer such as spruce_causal_topk that reads only j <= i); causal = 0: all.
  * qp [S, Qb, Pq, P], kp [S, Kb, Pk, P], scores [S, Qb, Kb] contiguous.
  * Replaces FlatGate.forward (selector/gate.py:29-101) plus the causal mask of
  * selector/recall.py:26-35.

@@ -224,30 +224,53 @@ __global__ __launch_bounds__(256) void project_kernel(const float* __restrict__ 
 }
 
 // Vector form for D % 4 == 0, P % 4 == 0 and 16-byte aligned operands: a
-// 64 x 64 output tile per workgroup, a 4 x 4 register tile per thread, x
-// staged transposed so every step reads one float4 of x and one of w from
-// LDS for 16 FMAs (the scalar form above reads 3 values for 8).  Same
+// 16TR x 64 output tile per workgroup, a TR x 4 register tile per thread, x
+// staged transposed so every step reads TR floats of x and one float4 of w
+// from LDS for 4TR FMAs (the scalar form above reads 3 values for 8).  Same
 // fmaf chain per output (d in order from 0), so the results are identical.
-constexpr int kVR = 64, kVC = 64, kVD = 128;
-__global__ __launch_bounds__(256) void project_tile_kernel(const float* __restrict__ x, const float* __restrict__ w,
-                                                           int64_t N, int D, int P, float* __restrict__ out) {
-  __shared__ __attribute__((aligned(16))) float xs[kVD][kVR + 4];
+// One launch can carry two projections (the query and key prototypes of the
+// selector): row tiles [0, tiles_a) belong to problem a, the rest to b.
+constexpr int kVC = 64, kVD = 128;
+struct ProjPair {
+  const float* xa;
+  const float* wa;
+  float* outa;
+  const float* xb;
+  const float* wb;
+  float* outb;
+  int64_t na, nb, tiles_a;
+  int D, P;
+};
+
+template <int TR>
+__global__ __launch_bounds__(256) void project_tile_kernel(const ProjPair pp) {
+  constexpr int R = 16 * TR;   // rows per tile
+  constexpr int XL = R / 8;    // float4 of x per thread per slice
+  __shared__ __attribute__((aligned(16))) float xs[kVD][R + 4];
   __shared__ __attribute__((aligned(16))) float ws[kVD][kVC];
+  const bool second = (int64_t)blockIdx.x >= pp.tiles_a;
+  const float* __restrict__ x = second ? pp.xb : pp.xa;
+  const float* __restrict__ w = second ? pp.wb : pp.wa;
+  float* __restrict__ out = second ? pp.outb : pp.outa;
+  const int64_t N = second ? pp.nb : pp.na;
+  const int D = pp.D, P = pp.P;
   const int tid = threadIdx.x;
   const int tr = tid >> 4, tc = tid & 15;
-  const int64_t n0 = (int64_t)blockIdx.x * kVR;
+  const int64_t n0 = ((int64_t)blockIdx.x - (second ? pp.tiles_a : 0)) * R;
   const int j0 = blockIdx.y * kVC;
-  float acc[4][4];
+  float acc[TR][4];
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int a = 0; a < TR; ++a)
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[a][c] = 0.f;
   for (int d0 = 0; d0 < D; d0 += kVD) {
     const int dn = D - d0 < kVD ? D - d0 : kVD;
-    float4 xv[8], wv[8];
+    float4 xv[XL], wv[8];
+    // x is staged row-fastest (lane r of a wave reads row r's float4), so the
+    // transposed LDS stores of a wave fall in distinct banks.
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const int e = tid + 256 * t, r = e >> 5, c4 = e & 31;
+    for (int t = 0; t < XL; ++t) {
+      const int e = tid + 256 * t, r = e % R, c4 = e / R;
       const int64_t n = n0 + r;
       xv[t] = (n < N && 4 * c4 < dn) ? *reinterpret_cast<const float4*>(x + n * D + d0 + 4 * c4)
                                      : float4{0.f, 0.f, 0.f, 0.f};
@@ -261,8 +284,8 @@ __global__ __launch_bounds__(256) void project_tile_kernel(const float* __restri
     }
     if (d0 > 0) __syncthreads();  // the previous slice's reads are done
 #pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const int e = tid + 256 * t, r = e >> 5, c4 = e & 31;
+    for (int t = 0; t < XL; ++t) {
+      const int e = tid + 256 * t, r = e % R, c4 = e / R;
       xs[4 * c4][r] = xv[t].x;
       xs[4 * c4 + 1][r] = xv[t].y;
       xs[4 * c4 + 2][r] = xv[t].z;
@@ -276,11 +299,17 @@ __global__ __launch_bounds__(256) void project_tile_kernel(const float* __restri
     __syncthreads();
 #pragma unroll 4
     for (int dd = 0; dd < dn; ++dd) {
-      const float4 a4 = *reinterpret_cast<const float4*>(&xs[dd][4 * tr]);
-      const float4 b4 = *reinterpret_cast<const float4*>(&ws[dd][4 * tc]);
-      const float av[4] = {a4.x, a4.y, a4.z, a4.w}, bv[4] = {b4.x, b4.y, b4.z, b4.w};
+      float av[TR];
 #pragma unroll
-      for (int a = 0; a < 4; ++a)
+      for (int a = 0; a < TR; a += 2) {
+        const float2 a2 = *reinterpret_cast<const float2*>(&xs[dd][TR * tr + a]);
+        av[a] = a2.x;
+        av[a + 1] = a2.y;
+      }
+      const float4 b4 = *reinterpret_cast<const float4*>(&ws[dd][4 * tc]);
+      const float bv[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+      for (int a = 0; a < TR; ++a)
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[a][c] = __builtin_fmaf(av[a], bv[c], acc[a][c]);
     }
@@ -288,8 +317,8 @@ __global__ __launch_bounds__(256) void project_tile_kernel(const float* __restri
   const int j = j0 + 4 * tc;
   if (j >= P) return;
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const int64_t n = n0 + 4 * tr + a;
+  for (int a = 0; a < TR; ++a) {
+    const int64_t n = n0 + TR * tr + a;
     if (n < N) *reinterpret_cast<float4*>(out + n * P + j) = float4{acc[a][0], acc[a][1], acc[a][2], acc[a][3]};
   }
 }
@@ -404,7 +433,7 @@ struct ScoreParams {
   float* scores;    // [BG, Qb, Kb]
   int Qb, Kb, Pq, Pk, P;
   float div;
-  int causal;  // 1: j > i is -inf and not computed
+  int causal;  // 1: j > i is -inf and not computed; 2 (Qb == Kb): j > i unspecified
 };
 
 // Copies n float4 from src to LDS dst (dst index = map(e)), 8 loads in flight
@@ -493,25 +522,47 @@ __global__ __launch_bounds__(256) void gate_scores_kernel(const ScoreParams p) {
 }
 
 // The same scores, register-blocked, for one query prototype and PK (1 or 2)
-// key prototypes: a workgroup covers 64 query blocks x 64 key blocks and
-// thread (tr, tc) holds query blocks 4tr..4tr+3 x key blocks 4tc..4tc+3 for
-// every key prototype. The prototypes are staged transposed ([e][block]) in
-// slices of kGS dims, so each step over e reads one float4 of query values
-// and PK float4 of key values for 16 * PK fmaf (the kernel above reads five
-// float4 for 16). Same operation order as the kernel above.
-constexpr int kGT = 64, kGS = 32, kGRow = kGT + 4;  // tile, slice, padded LDS row (floats)
-template <int PK>
+// key prototypes: a workgroup covers 16TR query blocks x 64 key blocks and
+// thread (tr, tc) holds query blocks TR*tr..TR*tr+TR-1 x key blocks
+// 4tc..4tc+3 for every key prototype. The prototypes are staged transposed
+// ([e][block]) in slices of kGS dims, so each step over e reads TR query
+// values and PK float4 of key values for 4 * TR * PK fmaf (the kernel above
+// reads five float4 for 16). Same operation order as the kernel above.
+constexpr int kGT = 64, kGS = 32;  // key tile, slice of the projection dim
+constexpr int kScoreTR = 2;        // query blocks per thread (tile of 16 * kScoreTR)
+template <int PK, int TR>
 __global__ __launch_bounds__(256) void gate_scores_tile_kernel(const ScoreParams p) {
-  __shared__ __attribute__((aligned(16))) float xs[kGS * kGRow];
-  __shared__ __attribute__((aligned(16))) float ys[PK * kGS * kGRow];
-  const int bg = blockIdx.z;
-  const int i0 = blockIdx.x * kGT, j0 = blockIdx.y * kGT;
+  constexpr int R = 16 * TR;               // query blocks per tile
+  constexpr int kXRow = R + 4, kYRow = kGT + 4;  // padded LDS rows (floats)
+  constexpr int kBands = kGT / R;          // query tiles per 64-block band
+  __shared__ __attribute__((aligned(16))) float xs[kGS * kXRow];
+  __shared__ __attribute__((aligned(16))) float ys[PK * kGS * kYRow];
+  int bg, i0, j0;
+  if (p.causal == 2) {
+    // 1-D grid over the tiles on or below the diagonal (Qb == Kb).  Band m
+    // (query blocks 64m..64m+63) holds kBands query tiles of m + 1 key tiles
+    // each, kBands * m(m+1)/2 tiles before it.
+    const int nt = (p.Qb + kGT - 1) / kGT, ntri = kBands * (nt * (nt + 1) / 2);
+    bg = blockIdx.x / ntri;
+    const int t = blockIdx.x - bg * ntri;
+    int m = (int)((sqrtf(8.f * (float)t / kBands + 1.f) - 1.f) * 0.5f);
+    while (kBands * ((m + 1) * (m + 2) / 2) <= t) ++m;
+    while (kBands * (m * (m + 1) / 2) > t) --m;
+    const int rem = t - kBands * (m * (m + 1) / 2);
+    const int h = rem / (m + 1);
+    i0 = (m * kBands + h) * R;
+    j0 = (rem - h * (m + 1)) * kGT;
+  } else {
+    bg = blockIdx.z;
+    i0 = blockIdx.x * R;
+    j0 = blockIdx.y * kGT;
+  }
   const int tid = threadIdx.x, tr = tid >> 4, tc = tid & 15;
   float* out = p.scores + (int64_t)bg * p.Qb * p.Kb;
-  if (p.causal && j0 > i0 + kGT - 1) {
+  if (p.causal && j0 > i0 + R - 1) {
     // Entirely above the diagonal.
-    for (int r = 0; r < 4; ++r) {
-      const int i = i0 + 4 * tr + r;
+    for (int r = 0; r < TR; ++r) {
+      const int i = i0 + TR * tr + r;
       for (int k = 0; k < 4; ++k) {
         const int j = j0 + 4 * tc + k;
         if (i < p.Qb && j < p.Kb) out[(int64_t)i * p.Kb + j] = -INFINITY;
@@ -521,66 +572,87 @@ __global__ __launch_bounds__(256) void gate_scores_tile_kernel(const ScoreParams
   }
   const float* qsrc = p.qp + (int64_t)bg * p.Qb * p.P;
   const float* ksrc = p.kp + (int64_t)bg * p.Kb * PK * p.P;
-  float acc[PK][4][4];
+  float acc[PK][TR][4];
 #pragma unroll
   for (int c = 0; c < PK; ++c)
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < TR; ++r)
 #pragma unroll
       for (int k = 0; k < 4; ++k) acc[c][r][k] = 0.f;
   // Staging map: kD4 consecutive lanes read one block's slice (contiguous).
   constexpr int kD4 = kGS / 4;                  // float4 per block slice
-  constexpr int kLoads = kGT * kD4 / 256;       // float4 per thread per operand
-  for (int e0 = 0; e0 < p.P; e0 += kGS) {
-    float4 qv[kLoads], kv[PK][kLoads];
+  constexpr int kLoadsQ = R * kD4 / 256;        // query float4 per thread
+  constexpr int kLoads = kGT * kD4 / 256;       // key float4 per thread per prototype
+  // The next slice's operands are loaded into registers while the current
+  // slice is consumed from LDS.
+  float4 qv[kLoadsQ], kv[PK][kLoads];
+  auto load_slice = [&](int e0) {
+#pragma unroll
+    for (int t = 0; t < kLoadsQ; ++t) {
+      const int idx = tid + 256 * t, blk = idx / kD4, d4 = idx % kD4;
+      const int i = i0 + blk;
+      qv[t] = i < p.Qb ? *reinterpret_cast<const float4*>(qsrc + (int64_t)i * p.P + e0 + 4 * d4)
+                       : float4{0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
     for (int t = 0; t < kLoads; ++t) {
       const int idx = tid + 256 * t, blk = idx / kD4, d4 = idx % kD4;
-      const int i = i0 + blk, j = j0 + blk;
-      qv[t] = i < p.Qb ? *reinterpret_cast<const float4*>(qsrc + (int64_t)i * p.P + e0 + 4 * d4)
-                       : float4{0.f, 0.f, 0.f, 0.f};
+      const int j = j0 + blk;
 #pragma unroll
       for (int c = 0; c < PK; ++c)
         kv[c][t] = j < p.Kb ? *reinterpret_cast<const float4*>(ksrc + ((int64_t)j * PK + c) * p.P + e0 + 4 * d4)
                             : float4{0.f, 0.f, 0.f, 0.f};
     }
+  };
+  load_slice(0);
+  for (int e0 = 0; e0 < p.P; e0 += kGS) {
     __syncthreads();  // the previous slice has been read
+#pragma unroll
+    for (int t = 0; t < kLoadsQ; ++t) {
+      const int idx = tid + 256 * t, blk = idx / kD4, d4 = idx % kD4;
+      float* x = xs + 4 * d4 * kXRow + blk;
+      x[0] = qv[t].x;
+      x[kXRow] = qv[t].y;
+      x[2 * kXRow] = qv[t].z;
+      x[3 * kXRow] = qv[t].w;
+    }
 #pragma unroll
     for (int t = 0; t < kLoads; ++t) {
       const int idx = tid + 256 * t, blk = idx / kD4, d4 = idx % kD4;
-      float* x = xs + 4 * d4 * kGRow + blk;
-      x[0] = qv[t].x;
-      x[kGRow] = qv[t].y;
-      x[2 * kGRow] = qv[t].z;
-      x[3 * kGRow] = qv[t].w;
 #pragma unroll
       for (int c = 0; c < PK; ++c) {
-        float* y = ys + (c * kGS + 4 * d4) * kGRow + blk;
+        float* y = ys + (c * kGS + 4 * d4) * kYRow + blk;
         y[0] = kv[c][t].x;
-        y[kGRow] = kv[c][t].y;
-        y[2 * kGRow] = kv[c][t].z;
-        y[3 * kGRow] = kv[c][t].w;
+        y[kYRow] = kv[c][t].y;
+        y[2 * kYRow] = kv[c][t].z;
+        y[3 * kYRow] = kv[c][t].w;
       }
     }
     __syncthreads();
+    if (e0 + kGS < p.P) load_slice(e0 + kGS);
 #pragma unroll 8
     for (int e = 0; e < kGS; ++e) {
-      const float4 x4 = *reinterpret_cast<const float4*>(xs + e * kGRow + 4 * tr);
-      const float x[4] = {x4.x, x4.y, x4.z, x4.w};
+      float x[TR];
+#pragma unroll
+      for (int r = 0; r < TR; r += 2) {
+        const float2 x2 = *reinterpret_cast<const float2*>(xs + e * kXRow + TR * tr + r);
+        x[r] = x2.x;
+        x[r + 1] = x2.y;
+      }
 #pragma unroll
       for (int c = 0; c < PK; ++c) {
-        const float4 y4 = *reinterpret_cast<const float4*>(ys + (c * kGS + e) * kGRow + 4 * tc);
+        const float4 y4 = *reinterpret_cast<const float4*>(ys + (c * kGS + e) * kYRow + 4 * tc);
         const float y[4] = {y4.x, y4.y, y4.z, y4.w};
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+        for (int r = 0; r < TR; ++r)
 #pragma unroll
           for (int k = 0; k < 4; ++k) acc[c][r][k] = __builtin_fmaf(x[r], y[k], acc[c][r][k]);
       }
     }
   }
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int i = i0 + 4 * tr + r;
+  for (int r = 0; r < TR; ++r) {
+    const int i = i0 + TR * tr + r;
     if (i >= p.Qb) continue;
     float v[4];
 #pragma unroll
@@ -707,9 +779,10 @@ __global__ __launch_bounds__(256) void causal_topk_kernel(const float* __restric
 // Causal top-k with one wavefront per row (rows up to kWaveTopkKb keys): each
 // lane holds keys j = lane + 64 s in registers.  A 32-step binary search over
 // order keys finds the k-th largest key T (the largest T with at least k keys
-// >= T), counting with ballots; then an in-order compaction takes every key
-// above T and the lowest-index keys equal to it.  Same result as
-// causal_topk_kernel, without LDS atomics or a serial bin scan.
+// >= T), counting with ballots, or any T with exactly k keys >= T; then an
+// in-order compaction takes every key above T and the lowest-index keys equal
+// to it.  Same result as causal_topk_kernel, without LDS atomics or a serial
+// bin scan.
 constexpr int kWaveTopkKb = 1024;
 constexpr int kWaveTopkPer = kWaveTopkKb / 64;
 __global__ __launch_bounds__(256) void causal_topk_wave_kernel(const float* __restrict__ scores, int64_t rows,
@@ -731,6 +804,10 @@ __global__ __launch_bounds__(256) void causal_topk_wave_kernel(const float* __re
     const int j = lane + 64 * s;
     key[s] = j < n ? order_key(srow[j] + 0.0f) : 0u;  // -0 -> +0; absent keys rank below all
   }
+  // The search stops early once exactly k keys are >= the candidate: those k
+  // keys are then the top k (the k-th largest is >= it and the (k+1)-th is
+  // below), and the compaction below takes exactly them, as it would with the
+  // k-th largest key itself as T.
   uint32_t T = 0;
   for (int bit = 31; bit >= 0; --bit) {
     const uint32_t cand = T | (1u << bit);
@@ -738,6 +815,7 @@ __global__ __launch_bounds__(256) void causal_topk_wave_kernel(const float* __re
 #pragma unroll
     for (int s = 0; s < kWaveTopkPer; ++s) cnt += __popcll(__ballot(key[s] >= cand));
     if (cnt >= k) T = cand;
+    if (cnt == k) break;
   }
   int gt = 0;
 #pragma unroll
@@ -819,11 +897,12 @@ extern "C" int spruce_gate_project(const float* x, const float* w, int64_t N, in
     return check_launch("project_block_kernel");
   }
   if (vec) {
-    const int64_t vrows = (N + kVR - 1) / kVR;
+    const int64_t vrows = (N + 63) / 64;
     SPRUCE_REQUIRE(vrows < ((int64_t)1 << 31) && P < ((int64_t)1 << 20) && D < ((int64_t)1 << 20),
                    "projection too large");
-    hipLaunchKernelGGL(project_tile_kernel, dim3((unsigned)vrows, (unsigned)((P + kVC - 1) / kVC)), dim3(256), 0,
-                       (hipStream_t)stream, x, w, N, (int)D, (int)P, out);
+    const ProjPair pp{x, w, out, nullptr, nullptr, nullptr, N, 0, vrows, (int)D, (int)P};
+    hipLaunchKernelGGL(project_tile_kernel<4>, dim3((unsigned)vrows, (unsigned)((P + kVC - 1) / kVC)), dim3(256), 0,
+                       (hipStream_t)stream, pp);
     return check_launch("project_tile_kernel");
   }
   const int64_t rows = (N + kPR - 1) / kPR;
@@ -832,6 +911,30 @@ extern "C" int spruce_gate_project(const float* x, const float* w, int64_t N, in
   hipLaunchKernelGGL(project_kernel, dim3((unsigned)rows, (unsigned)((P + kPC - 1) / kPC)), dim3(256), 0,
                      (hipStream_t)stream, x, w, N, (int)D, (int)P, out);
   return check_launch("project_kernel");
+}
+
+// Both selector projections in one launch (32-row tiles: at the selector's
+// sizes the single-problem launches leave most CUs idle); shapes outside the
+// vector form or large enough for the block kernel take two launches.
+extern "C" int spruce_gate_project2(const float* xa, const float* wa, int64_t Na, const float* xb, const float* wb,
+                                    int64_t Nb, int64_t D, int64_t P, float* outa, float* outb, void* stream) {
+  SPRUCE_REQUIRE(xa && wa && outa && xb && wb && outb, "x, w and out of both projections must be non-null");
+  SPRUCE_REQUIRE(Na >= 1 && Nb >= 1 && D >= 1 && P >= 1 && (Na + Nb) * P < ((int64_t)1 << 40),
+                 "invalid projection shape");
+  auto aligned = [](const void* q) { return ((uintptr_t)q % 16) == 0; };
+  const bool vec = D % 4 == 0 && P % 4 == 0 && aligned(xa) && aligned(wa) && aligned(outa) && aligned(xb) &&
+                   aligned(wb) && aligned(outb);
+  if (!vec || Na >= kBlockProjectRows || Nb >= kBlockProjectRows) {
+    const int rc = spruce_gate_project(xa, wa, Na, D, P, outa, stream);
+    return rc != 0 ? rc : spruce_gate_project(xb, wb, Nb, D, P, outb, stream);
+  }
+  SPRUCE_REQUIRE(P < ((int64_t)1 << 20) && D < ((int64_t)1 << 20), "projection too large");
+  constexpr int TR = 2, R = 16 * TR;
+  const int64_t ta = (Na + R - 1) / R, tb = (Nb + R - 1) / R;
+  const ProjPair pp{xa, wa, outa, xb, wb, outb, Na, Nb, ta, (int)D, (int)P};
+  hipLaunchKernelGGL(project_tile_kernel<TR>, dim3((unsigned)(ta + tb), (unsigned)((P + kVC - 1) / kVC)), dim3(256),
+                     0, (hipStream_t)stream, pp);
+  return check_launch("project_tile_kernel");
 }
 
 extern "C" int spruce_gate_scores(const float* qp, const float* kp, int64_t BG, int64_t Qb, int64_t Kb, int64_t Pq,
@@ -843,7 +946,8 @@ extern "C" int spruce_gate_scores(const float* qp, const float* kp, int64_t BG, 
                  "qp and kp must be 16-byte aligned");
   SPRUCE_REQUIRE(BG < 65536 && Qb < (1 << 30) && Kb < (1 << 30) && Pq * Pk * P < ((int64_t)1 << 30),
                  "score shape out of range");
-  ScoreParams p{qp, kp, scores, (int)Qb, (int)Kb, (int)Pq, (int)Pk, (int)P, div, causal ? 1 : 0};
+  SPRUCE_REQUIRE(causal >= 0 && causal <= 2, "causal must be 0, 1 or 2, got %d", causal);
+  ScoreParams p{qp, kp, scores, (int)Qb, (int)Kb, (int)Pq, (int)Pk, (int)P, div, causal};
   const int64_t lds = (int64_t)(kTI * Pq * P + kTJ * (Pk * P + 4)) * 4;
   if (lds > 160 * 1024) {
     const int64_t total = BG * Qb * Kb;
@@ -853,12 +957,21 @@ extern "C" int spruce_gate_scores(const float* qp, const float* kp, int64_t BG, 
                        total);
     return check_launch("gate_scores_direct_kernel");
   }
+  const bool tri = causal == 2 && Qb == Kb;
+  if (!tri && causal == 2) p.causal = 1;
   if (Pq == 1 && (Pk == 1 || Pk == 2) && P % kGS == 0 && reinterpret_cast<uintptr_t>(scores) % 16 == 0) {
-    const dim3 grid((unsigned)((Qb + kGT - 1) / kGT), (unsigned)((Kb + kGT - 1) / kGT), (unsigned)BG);
+    // 32-query-block tiles: twice as many workgroups as 64-block tiles,
+    // which evens out the per-CU share of a few hundred tiles.
+    constexpr int TR = kScoreTR, R = 16 * TR;
+    const int64_t nt = (Qb + kGT - 1) / kGT;
+    const int64_t ntri = (kGT / R) * (nt * (nt + 1) / 2);
+    SPRUCE_REQUIRE(!tri || BG * ntri < ((int64_t)1 << 31), "score matrix too large");
+    const dim3 grid = tri ? dim3((unsigned)(BG * ntri))
+                          : dim3((unsigned)((Qb + R - 1) / R), (unsigned)((Kb + kGT - 1) / kGT), (unsigned)BG);
     if (Pk == 1)
-      hipLaunchKernelGGL(gate_scores_tile_kernel<1>, grid, dim3(256), 0, (hipStream_t)stream, p);
+      hipLaunchKernelGGL((gate_scores_tile_kernel<1, TR>), grid, dim3(256), 0, (hipStream_t)stream, p);
     else
-      hipLaunchKernelGGL(gate_scores_tile_kernel<2>, grid, dim3(256), 0, (hipStream_t)stream, p);
+      hipLaunchKernelGGL((gate_scores_tile_kernel<2, TR>), grid, dim3(256), 0, (hipStream_t)stream, p);
     return check_launch("gate_scores_tile_kernel");
   }
   const dim3 grid((unsigned)((Qb + kTI - 1) / kTI), (unsigned)((Kb + kTJ - 1) / kTJ), (unsigned)BG);

@@ -83,10 +83,38 @@ def project(x, W):
     return out.reshape(x.shape[:-1] + (P,))
 
 
+def project_pair(xa, Wa, xb, Wb):
+    """``project(xa, Wa), project(xb, Wb)`` in one launch (same results)."""
+    _cuda(xa, "xa")
+    _cuda(xb, "xb")
+    for x, W in ((xa, Wa), (xb, Wb)):
+        if x.dtype != torch.float32 or W.dtype != torch.float32:
+            raise ValueError("projection inputs must be float32")
+        if W.dim() != 2 or x.shape[-1] != W.shape[0]:
+            raise ValueError(f"shape mismatch: x {tuple(x.shape)} @ W {tuple(W.shape)}")
+    if Wa.shape != Wb.shape:
+        raise ValueError("the two projections must share [D, P]")
+    xa2 = xa.reshape(-1, xa.shape[-1]).contiguous()
+    xb2 = xb.reshape(-1, xb.shape[-1]).contiguous()
+    Wa = Wa.to(xa.device).contiguous()
+    Wb = Wb.to(xa.device).contiguous()
+    D, P = Wa.shape
+    oa = torch.empty((xa2.shape[0], P), device=xa.device, dtype=torch.float32)
+    ob = torch.empty((xb2.shape[0], P), device=xa.device, dtype=torch.float32)
+    with torch.cuda.device(xa.device):
+        rc = spruce_hip.lib().spruce_gate_project2(
+            spruce_hip.ptr(xa2), spruce_hip.ptr(Wa), xa2.shape[0], spruce_hip.ptr(xb2), spruce_hip.ptr(Wb),
+            xb2.shape[0], D, P, spruce_hip.ptr(oa), spruce_hip.ptr(ob), spruce_hip.stream_of(xa))
+    spruce_hip.check(rc, "spruce_gate_project2")
+    return oa.reshape(xa.shape[:-1] + (P,)), ob.reshape(xb.shape[:-1] + (P,))
+
+
 def gate_scores(qp, kp, causal=True, div=None):
     """MaxSim scores ``[S, Qb, Kb]`` from projected prototypes ``qp [S,Qb,Pq,P]``
     and ``kp [S,Kb,Pk,P]``, divided by ``div`` (default sqrt(P)); with
-    ``causal`` the entries above the diagonal are -inf."""
+    ``causal`` the entries above the diagonal are -inf.  ``causal="lower"``
+    (Qb == Kb) computes only j <= i and leaves the entries above the diagonal
+    unspecified, for consumers that read only the causal part."""
     _cuda(qp, "qp")
     if qp.dim() != 4 or kp.dim() != 4 or qp.shape[0] != kp.shape[0] or qp.shape[3] != kp.shape[3]:
         raise ValueError("qp must be [S,Qb,Pq,P] and kp [S,Kb,Pk,P]")
@@ -100,7 +128,8 @@ def gate_scores(qp, kp, causal=True, div=None):
     out = torch.empty((S, Qb, Kb), device=qp.device, dtype=torch.float32)
     with torch.cuda.device(qp.device):
         rc = spruce_hip.lib().spruce_gate_scores(
-            spruce_hip.ptr(qp), spruce_hip.ptr(kp), S, Qb, Kb, Pq, Pk, P, d, int(bool(causal)),
+            spruce_hip.ptr(qp), spruce_hip.ptr(kp), S, Qb, Kb, Pq, Pk, P, d,
+            2 if causal == "lower" else int(bool(causal)),
             spruce_hip.ptr(out), spruce_hip.stream_of(qp))
     spruce_hip.check(rc, "spruce_gate_scores")
     return out
@@ -139,10 +168,14 @@ def select_blocks(query, key, Wq, Wk, top_k=32, return_intermediates=False):
     """
     q_mean, k_sum = pool_blocks(query, key)
     B, Hkv, nb, D = q_mean.shape
-    qp = project(q_mean, Wq)                       # [B,Hkv,nb,P]
-    kp = project(k_sum, Wk)                        # [B,Hkv,nb,2,P]
+    if Wq.shape == Wk.shape:
+        qp, kp = project_pair(q_mean, Wq, k_sum, Wk)   # [B,Hkv,nb,P], [B,Hkv,nb,2,P]
+    else:
+        qp, kp = project(q_mean, Wq), project(k_sum, Wk)
     P = qp.shape[-1]
-    sc = gate_scores(qp.reshape(B * Hkv, nb, 1, P), kp.reshape(B * Hkv, nb, 2, P), causal=True)
+    # The top-k reads only j <= i; the intermediates keep the -inf fill.
+    sc = gate_scores(qp.reshape(B * Hkv, nb, 1, P), kp.reshape(B * Hkv, nb, 2, P),
+                     causal=True if return_intermediates else "lower")
     sel = causal_topk_blocks(sc, top_k).reshape(B, Hkv, nb, top_k)[:, None]
     if not return_intermediates:
         return sel

@@ -10,7 +10,7 @@ import torch
 
 import oracle.selector as osel
 from selector.gate import FlatGate
-from selector.select import causal_topk_blocks, gate_scores, pool_blocks, project, select_blocks
+from selector.select import causal_topk_blocks, gate_scores, pool_blocks, project, project_pair, select_blocks
 from spruce_hip import workloads
 
 pytestmark = pytest.mark.gpu
@@ -67,6 +67,43 @@ def test_projection_shapes_are_bit_exact(N, D, P):
     W = torch.randn(D, P, generator=gen) * 0.1
     got = project(x.to(DEV), W)
     assert np.array_equal(_np(got), osel.project(x.numpy(), W.numpy()))
+
+
+@pytest.mark.parametrize("Na,Nb,D,P", [
+    (4096, 8192, 128, 128),   # cfg3: query and key prototypes of 4 KV heads x 1024 blocks
+    (77, 130, 96, 36),        # ragged 32-row tiles and 64-column tiles
+    (1, 33, 128, 64),
+    (5, 7, 6, 5),             # scalar form: two launches
+    (20000, 100, 128, 128),   # block kernel for the large side: two launches
+])
+def test_projection_pair_equals_single_launches(Na, Nb, D, P):
+    gen = torch.Generator().manual_seed(Na + Nb + D)
+    xa, xb = torch.randn(Na, D, generator=gen), torch.randn(Nb, D, generator=gen)
+    Wa, Wb = torch.randn(D, P, generator=gen) * 0.1, torch.randn(D, P, generator=gen) * 0.1
+    oa, ob = project_pair(xa.to(DEV), Wa.to(DEV), xb.to(DEV), Wb.to(DEV))
+    assert np.array_equal(_np(oa), osel.project(xa.numpy(), Wa.numpy()))
+    assert np.array_equal(_np(ob), osel.project(xb.numpy(), Wb.numpy()))
+    assert torch.equal(oa, project(xa.to(DEV), Wa)) and torch.equal(ob, project(xb.to(DEV), Wb))
+
+
+@pytest.mark.parametrize("S,Qb,Pk,P", [
+    (2, 130, 2, 128),    # triangular tile grid, ragged last tile
+    (4, 1024, 2, 128),   # cfg3 score shape
+    (1, 64, 1, 64),
+    (1, 1, 2, 128),
+    (1, 200, 2, 48),     # P % 32 != 0: the broadcast kernel (full -inf fill)
+])
+def test_lower_scores_equal_the_causal_fill_on_and_below_the_diagonal(S, Qb, Pk, P):
+    # causal="lower" launches only the tiles on or below the diagonal; the
+    # causal entries must equal the fully filled causal matrix bit for bit.
+    gen = torch.Generator().manual_seed(Qb + P)
+    qp = torch.randn(S, Qb, 1, P, generator=gen).to(DEV)
+    kp = torch.randn(S, Qb, Pk, P, generator=gen).to(DEV)
+    full = gate_scores(qp, kp, causal=True)
+    lower = gate_scores(qp, kp, causal="lower")
+    tril = torch.tril(torch.ones(Qb, Qb, dtype=torch.bool, device=DEV))
+    assert torch.equal(full[:, tril], lower[:, tril])
+    assert torch.equal(causal_topk_blocks(lower, 16), causal_topk_blocks(full, 16))
 
 
 @pytest.mark.parametrize("S,Qb,Kb,Pk,P", [
@@ -173,3 +210,7 @@ def test_cfg3_full_size_selected_blocks_bit_exact():
     assert np.all(np.diff(rows, axis=1)[both] > 0)              # strictly increasing
     assert np.all(~valid[:, 1:] | valid[:, :-1])                # padding only trailing
     assert valid.reshape(4, 1024, 32)[:, 31:].all()             # >= 32 causal blocks: full rows
+    # The production path (paired projection, scores on and below the diagonal only).
+    fast = select_blocks(q.transpose(1, 2).contiguous().to(DEV).transpose(1, 2), k.to(DEV),
+                         Wq.to(DEV), Wk.to(DEV), top_k=32)
+    assert np.array_equal(_np(fast), exp["selected"])
