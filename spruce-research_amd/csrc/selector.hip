@@ -153,6 +153,175 @@ __global__ __launch_bounds__(256) void block_pool_kernel(const PoolParams p) {
   }
 }
 
+// 8 consecutive elements of TIn as raw bits, widened after the load returns.
+template <typename TIn>
+struct Raw8 {
+  uint4 a;
+};
+template <>
+struct Raw8<InF32> {
+  float4 a, b;
+};
+
+template <typename TIn>
+__device__ __forceinline__ Raw8<TIn> raw8_at(const void* base, int64_t elem) {
+  Raw8<TIn> r;
+  if constexpr (TIn::bytes == 4) {
+    const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(base) + elem);
+    r.a = q[0];
+    r.b = q[1];
+  } else {
+    r.a = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + elem);
+  }
+  return r;
+}
+
+template <typename TIn>
+__device__ __forceinline__ void widen8(const Raw8<TIn>& r, float* out) {
+  if constexpr (TIn::bytes == 4) {
+    out[0] = r.a.x; out[1] = r.a.y; out[2] = r.a.z; out[3] = r.a.w;
+    out[4] = r.b.x; out[5] = r.b.y; out[6] = r.b.z; out[7] = r.b.w;
+  } else {
+    constexpr bool F16 = TIn::code == SPRUCE_DTYPE_F16;
+    const uint32_t w[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = unpack1<F16>(w[i] & 0xffffu);
+      out[2 * i + 1] = unpack1<F16>(w[i] >> 16);
+    }
+  }
+}
+
+// block_pool_kernel with every load issued ahead of its use: the input type
+// is a template parameter (no per-load dtype branch), the G heads of a token
+// step are loaded together (G <= kPoolMaxG), and the K rows of the thread's
+// token steps (at most kPoolMaxPer) are loaded before the Q part starts.
+// Identical arithmetic: per token the heads summed left to right, token steps
+// folded in order, the same halving tree, the same divisions.
+constexpr int kPoolMaxG = 8, kPoolMaxPer = 8;
+template <typename TIn>
+__global__ __launch_bounds__(256) void block_pool_fast_kernel(const PoolParams p) {
+  __shared__ float red[256 * 8];
+  __shared__ float redmax[256 * 8];
+  const int dch = p.D / 8;
+  const int L = (256 / dch) > kSelBlock ? kSelBlock : 256 / dch;
+  const int per = kSelBlock / L;
+  const int tid = threadIdx.x;
+  const int l = tid / dch, c = tid - (tid / dch) * dch;
+  int w = blockIdx.x;
+  const int blk = w % p.nb;
+  w /= p.nb;
+  const int g = w % p.Hkv;
+  const int b = w / p.Hkv;
+  const int t0 = blk * kSelBlock;
+  int n = p.T - t0;
+  n = n > kSelBlock ? kSelBlock : n;
+  const bool work = tid < dch * L;
+
+  Raw8<TIn> kr[kPoolMaxPer];
+  if (p.k && work) {
+#pragma unroll
+    for (int i = 0; i < kPoolMaxPer; ++i) {
+      const int t = t0 + l + i * L;
+      if (i < per && t < p.T)
+        kr[i] = raw8_at<TIn>(p.k, (int64_t)b * p.ks[0] + (int64_t)g * p.ks[1] + (int64_t)t * p.ks[2] + 8 * c);
+    }
+  }
+
+  if (p.q) {
+    float acc[8];
+    if (work) {
+      for (int i = 0; i < per; ++i) {
+        const int t = t0 + l + i * L;
+        float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (t < p.T) {
+          const int64_t e0 = (int64_t)b * p.qs[0] + (int64_t)(g * p.G) * p.qs[1] + (int64_t)t * p.qs[2] + 8 * c;
+          Raw8<TIn> qr[kPoolMaxG];
+#pragma unroll
+          for (int h = 0; h < kPoolMaxG; ++h)
+            if (h < p.G) qr[h] = raw8_at<TIn>(p.q, e0 + (int64_t)h * p.qs[1]);
+          widen8<TIn>(qr[0], s);
+#pragma unroll
+          for (int h = 1; h < kPoolMaxG; ++h) {
+            if (h < p.G) {
+              float x[8];
+              widen8<TIn>(qr[h], x);
+#pragma unroll
+              for (int e = 0; e < 8; ++e) s[e] = s[e] + x[e];
+            }
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = (i == 0) ? s[e] : acc[e] + s[e];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) red[(l * dch + c) * 8 + e] = acc[e];
+    }
+    __syncthreads();
+    for (int st = L / 2; st >= 1; st /= 2) {
+      if (work && l < st) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          red[(l * dch + c) * 8 + e] = red[(l * dch + c) * 8 + e] + red[((l + st) * dch + c) * 8 + e];
+      }
+      __syncthreads();
+    }
+    if (work && l == 0) {
+      const float den = (float)(p.G * n);
+      float* o = p.q_mean + (((int64_t)b * p.Hkv + g) * p.nb + blk) * p.D + 8 * c;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = red[c * 8 + e] / den;
+    }
+    __syncthreads();
+  }
+
+  if (p.k) {
+    float acc[8], mx[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mx[e] = -INFINITY;
+    if (work) {
+#pragma unroll
+      for (int i = 0; i < kPoolMaxPer; ++i) {
+        if (i >= per) break;
+        const int t = t0 + l + i * L;
+        float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (t < p.T) {
+          widen8<TIn>(kr[i], s);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) mx[e] = max_total(mx[e], s[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = (i == 0) ? s[e] : acc[e] + s[e];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        red[(l * dch + c) * 8 + e] = acc[e];
+        redmax[(l * dch + c) * 8 + e] = mx[e];
+      }
+    }
+    __syncthreads();
+    for (int st = L / 2; st >= 1; st /= 2) {
+      if (work && l < st) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          red[(l * dch + c) * 8 + e] = red[(l * dch + c) * 8 + e] + red[((l + st) * dch + c) * 8 + e];
+          redmax[(l * dch + c) * 8 + e] = max_total(redmax[(l * dch + c) * 8 + e], redmax[((l + st) * dch + c) * 8 + e]);
+        }
+      }
+      __syncthreads();
+    }
+    if (work && l == 0) {
+      const float den = (float)n;
+      float* o = p.k_sum + ((((int64_t)b * p.Hkv + g) * p.nb + blk) * 2) * p.D + 8 * c;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        o[e] = red[c * 8 + e] / den;
+        o[p.D + e] = redmax[c * 8 + e];
+      }
+    }
+  }
+}
+
 // out[n][j] = fmaf chain over d (in order, from 0) of x[n][d] * w[d][j].
 // A workgroup computes a 32 x 64 output tile, each thread a 2 x 4 register
 // tile; x and w are staged through LDS in 128-wide slices of d (one slice for
@@ -877,6 +1046,17 @@ extern "C" int spruce_selector_pool(const void* q, const int64_t qs[4], const vo
   p.k_sum = k_sum;
   const int64_t grid = B * Hkv * p.nb;
   SPRUCE_REQUIRE(grid < ((int64_t)1 << 31), "grid too large");
+  const int dch = (int)(D / 8);
+  const int L = (256 / dch) > kSelBlock ? kSelBlock : 256 / dch;
+  if (p.G <= kPoolMaxG && kSelBlock / L <= kPoolMaxPer) {
+    if (dtype == SPRUCE_DTYPE_BF16)
+      hipLaunchKernelGGL(block_pool_fast_kernel<InBF16>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, p);
+    else if (dtype == SPRUCE_DTYPE_F16)
+      hipLaunchKernelGGL(block_pool_fast_kernel<InF16>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, p);
+    else
+      hipLaunchKernelGGL(block_pool_fast_kernel<InF32>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, p);
+    return check_launch("block_pool_fast_kernel");
+  }
   hipLaunchKernelGGL(block_pool_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, p);
   return check_launch("block_pool_kernel");
 }

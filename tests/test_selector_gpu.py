@@ -26,6 +26,9 @@ def _np(t):
     (2, 8, 2, 200, 64, torch.float16),
     (1, 4, 4, 64, 128, torch.float32),
     (1, 12, 2, 129, 16, torch.bfloat16),
+    (1, 16, 2, 300, 256, torch.bfloat16),   # G = 8, 8 token steps per thread: the typed kernel's limits
+    (1, 18, 2, 150, 128, torch.float16),    # G = 9: the generic kernel
+    (1, 4, 2, 100, 512, torch.float32),     # 16 token steps per thread: the generic kernel
 ])
 def test_pooling_is_bit_exact(B, Hq, Hkv, T, D, dtype):
     gen = torch.Generator().manual_seed(T + D)
@@ -35,6 +38,8 @@ def test_pooling_is_bit_exact(B, Hq, Hkv, T, D, dtype):
     eqm, eks = osel.block_pool(q.float().numpy(), k.float().numpy())
     assert np.array_equal(_np(qm), eqm)
     assert np.array_equal(_np(ks), eks)
+    _, ks_only = pool_blocks(None, k.to(DEV))
+    assert torch.equal(ks_only, ks)
 
 
 def test_projection_scores_and_topk_are_bit_exact():
