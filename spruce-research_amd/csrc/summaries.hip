@@ -15,10 +15,11 @@
 //
 // Aligned rows (16-byte rows, contiguous last dim, D % 64 == 0, the usual case):
 // pyramid_kernel reads K and V once and builds the dyadic table (16-token
-// leaves, each level the pairwise sums of the one below) in the workspace;
-// range_sum adds, per (b, h, range), the partial leaves at the range ends and
-// the table entries covering the rest: one entry for a tree-node prototype
-// range.  Other layouts take a scalar path: per-64-token chunk sums, then each
+// leaves, each level the pairwise sums of the one below) in the workspace,
+// pyramid_top_kernel forms the small upper levels in one launch, and
+// range_pyr_kernel adds, per (b, h, range), the partial leaves at the range
+// ends and the table entries covering the rest: one entry for a tree-node
+// prototype range.  Other layouts take a scalar path: per-64-token chunk sums, then each
 // range adds its covered chunks one by one.  HBM-bound: K and V are read once.
 #include <math.h>
 
@@ -362,16 +363,69 @@ __global__ __launch_bounds__(kSumThreads) void pyramid_kernel(PyrParams pp, int 
   }
 }
 
-// One wavefront per (b, h, range): lane = (token lane tl = lane / 16, granule
-// lane gl = lane % 16).  Edge tokens and cover entries are dealt round-robin
-// to the 4 token lanes, which are then combined with cross-lane shuffles (no
-// LDS, no barriers).
+// The levels above `base` when level `base` holds at most kTopMax entries per
+// (b, h): one workgroup per (b, h, chunk of kTopCols table columns) loads the
+// chunk of every level-`base` entry into LDS and forms all higher levels there
+// (entry i of a level = entries 2i and 2i+1 below, a missing right neighbour
+// counted as 0, as in pyramid_kernel), writing each level to the table.
+constexpr int kTopMax = 256, kTopCols = 8;
+__global__ __launch_bounds__(kSumThreads) void pyramid_top_kernel(PyrParams pp, int base) {
+  __shared__ float buf[2][kTopMax * kTopCols];
+  __shared__ int cbuf[2][kTopMax];
+  const SumParams& p = pp.p;
+  const int W = 2 * p.D;
+  const int nchunk = W / kTopCols;
+  const int chunk = blockIdx.x % nchunk;
+  const int bh = blockIdx.x / nchunk;
+  const int b = bh / p.H, h = bh % p.H;
+  const bool counts = pp.pcnt != nullptr && h == 0 && chunk == 0;
+  float* table = pp.pyr + (int64_t)bh * pp.E * W + chunk * kTopCols;
+  int n = pp.n[base];
+  for (int idx = threadIdx.x; idx < n * kTopCols / 4; idx += kSumThreads) {
+    const int i = idx / (kTopCols / 4), c4 = idx % (kTopCols / 4);
+    reinterpret_cast<float4*>(buf[0])[idx] =
+        reinterpret_cast<const float4*>(table + (int64_t)(pp.off[base] + i) * W)[c4];
+  }
+  if (counts)
+    for (int i = threadIdx.x; i < n; i += kSumThreads) cbuf[0][i] = pp.pcnt[(int64_t)b * pp.E + pp.off[base] + i];
+  __syncthreads();
+  int cur = 0;
+  for (int L = base + 1; L < pp.levels; ++L) {
+    const int m = pp.n[L];
+    const float* in = buf[cur];
+    float* out = buf[cur ^ 1];
+    float* dst = table + (int64_t)pp.off[L] * W;
+    for (int idx = threadIdx.x; idx < m * kTopCols; idx += kSumThreads) {
+      const int i = idx / kTopCols, col = idx % kTopCols;
+      const float right = 2 * i + 1 < n ? in[(2 * i + 1) * kTopCols + col] : 0.f;
+      const float v = in[2 * i * kTopCols + col] + right;
+      out[idx] = v;
+      dst[(int64_t)i * W + col] = v;
+    }
+    if (counts)
+      for (int i = threadIdx.x; i < m; i += kSumThreads) {
+        const int c = cbuf[cur][2 * i] + (2 * i + 1 < n ? cbuf[cur][2 * i + 1] : 0);
+        cbuf[cur ^ 1][i] = c;
+        pp.pcnt[(int64_t)b * pp.E + pp.off[L] + i] = c;
+      }
+    __syncthreads();
+    cur ^= 1;
+    n = m;
+  }
+}
+
+// Four ranges per wavefront: 16-lane group grp = lane / 16 takes range item
+// 4 * wave + grp (item = (b, h, range)), lane gl = lane % 16 its granule
+// columns gl + 16k.  A group adds the partial leaves at the range ends and then
+// the table entries covering the rest, in that order; a tree-node prototype
+// range is a single entry.  No cross-lane traffic.
 template <typename In, int NK>
 __global__ __launch_bounds__(kSumThreads) void range_pyr_kernel(PyrParams pp) {
   const SumParams& p = pp.p;
   const int lane = threadIdx.x & 63;
-  const int64_t idx = (int64_t)blockIdx.x * (kSumThreads / 64) + (threadIdx.x >> 6);
-  if (idx >= (int64_t)p.B * p.H * p.R) return;  // whole wavefront
+  const int gl = lane & 15;
+  const int64_t idx = ((int64_t)blockIdx.x * (kSumThreads / 64) + (threadIdx.x >> 6)) * 4 + (lane >> 4);
+  if (idx >= (int64_t)p.B * p.H * p.R) return;  // no barrier follows
   const int r = (int)(idx % p.R);
   const int bh = (int)(idx / p.R);
   const int h = bh % p.H, b = bh / p.H;
@@ -391,7 +445,6 @@ __global__ __launch_bounds__(kSumThreads) void range_pyr_kernel(PyrParams pp) {
     tail_start = e;
   }
   const int nh = (int)(head_end - s), nt = (int)(e > tail_start ? e - tail_start : 0);
-  const int tl = lane >> 4, gl = lane & 15;
   const int W = 2 * p.D;
   float acc[NK][8];
 #pragma unroll
@@ -404,7 +457,7 @@ __global__ __launch_bounds__(kSumThreads) void range_pyr_kernel(PyrParams pp) {
     const char* row[NK];
     int64_t step[NK];
     granule_ptrs<In, NK>(p, b, h, gl, row, step);
-    for (int i = tl; i < nh + nt; i += 4) {
+    for (int i = 0; i < nh + nt; ++i) {
       const int64_t t = i < nh ? s + i : tail_start + (i - nh);
       if (valid && !valid[t]) continue;
       ++nvalid;
@@ -413,51 +466,32 @@ __global__ __launch_bounds__(kSumThreads) void range_pyr_kernel(PyrParams pp) {
     }
   }
   const float* table = pp.pyr + (int64_t)bh * pp.E * W;
-  int q = 0;
-  for (int64_t c = c0; c < c1; ++q) {
+  for (int64_t c = c0; c < c1;) {
     // Largest aligned power-of-two block of leaves starting at c inside [c, c1).
     int j = 63 - __builtin_clzll((unsigned long long)(c1 - c));
     if (c != 0) {
       const int a = __builtin_ctzll((unsigned long long)c);
       j = a < j ? a : j;
     }
-    if ((q & 3) == tl) {
-      const int64_t ent = pp.off[j] + (c >> j);
+    const int64_t ent = pp.off[j] + (c >> j);
 #pragma unroll
-      for (int k = 0; k < NK; ++k) add_f8(table + ent * W + 8 * (gl + 16 * k), acc[k]);
-      if (valid) nvalid += pp.pcnt[(int64_t)b * pp.E + ent];
-    }
+    for (int k = 0; k < NK; ++k) add_f8(table + ent * W + 8 * (gl + 16 * k), acc[k]);
+    if (valid) nvalid += pp.pcnt[(int64_t)b * pp.E + ent];
     c += (int64_t)1 << j;
   }
-#pragma unroll
-  for (int k = 0; k < NK; ++k)
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      acc[k][u] += __shfl_xor(acc[k][u], 16, 64);
-      acc[k][u] += __shfl_xor(acc[k][u], 32, 64);
-    }
-  int count = (int)(e - s);
-  if (valid) {
-    // Every granule lane of a token lane holds the same count: take gl = 0's.
-    int n = gl == 0 ? nvalid : 0;
-    n += __shfl_xor(n, 16, 64);
-    n += __shfl_xor(n, 32, 64);
-    count = __shfl(n, 0, 64);
-  }
+  const int count = valid ? nvalid : (int)(e - s);
   const float denom = count > 1 ? (float)count : 1.0f;
   const int64_t orow = (((int64_t)b * p.H + h) * p.R + r) * p.D;
-  if (tl == 0) {
-    const int G = p.D / 8;
+  const int G = p.D / 8;
 #pragma unroll
-    for (int k = 0; k < NK; ++k) {
-      const int gc = gl + 16 * k;
-      const int which = gc >= G, d0 = 8 * (which ? gc - G : gc);
-      float* o = (which ? p.values : p.keys) + orow + d0;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) o[u] = acc[k][u] / denom;
-    }
+  for (int k = 0; k < NK; ++k) {
+    const int gc = gl + 16 * k;
+    const int which = gc >= G, d0 = 8 * (which ? gc - G : gc);
+    float4* o = reinterpret_cast<float4*>((which ? p.values : p.keys) + orow + d0);
+    o[0] = make_float4(acc[k][0] / denom, acc[k][1] / denom, acc[k][2] / denom, acc[k][3] / denom);
+    o[1] = make_float4(acc[k][4] / denom, acc[k][5] / denom, acc[k][6] / denom, acc[k][7] / denom);
   }
-  if (h == 0 && lane == 0) {
+  if (h == 0 && gl == 0) {
     p.counts[(int64_t)b * p.R + r] = (float)count;
     p.log_counts[(int64_t)b * p.R + r] = count > 0 ? logf((float)count) : -__builtin_inff();
   }
@@ -468,12 +502,20 @@ int launch_dyadic(const PyrParams& pp, int64_t g2, hipStream_t stream) {
   const size_t lds = (size_t)(24 * 2 * pp.p.D) * sizeof(float) + 32 * sizeof(int);
   for (int src = -1; src < pp.levels - 1; src = src < 0 ? kFold : src + kFold) {
     const int64_t nb = pp.n[src < 0 ? 0 : src];
+    if (src >= 0 && nb <= kTopMax && (2 * pp.p.D) % kTopCols == 0) {
+      // Every level above src in one launch.
+      const int64_t grid = (int64_t)pp.p.B * pp.p.H * (2 * pp.p.D / kTopCols);
+      hipLaunchKernelGGL(pyramid_top_kernel, dim3((unsigned)grid), dim3(kSumThreads), 0, stream, pp, src);
+      const int rc = check_launch("pyramid_top_kernel");
+      if (rc) return rc;
+      break;
+    }
     const int64_t grid = (int64_t)pp.p.B * pp.p.H * ((nb + 15) / 16);
     hipLaunchKernelGGL((pyramid_kernel<In, NK>), dim3((unsigned)grid), dim3(kSumThreads), lds, stream, pp, src);
     const int rc = check_launch("pyramid_kernel");
     if (rc) return rc;
   }
-  const int64_t g3 = (g2 + kSumThreads / 64 - 1) / (kSumThreads / 64);
+  const int64_t g3 = (g2 + kSumThreads / 16 - 1) / (kSumThreads / 16);
   hipLaunchKernelGGL((range_pyr_kernel<In, NK>), dim3((unsigned)g3), dim3(kSumThreads), 0, stream, pp);
   return check_launch("range_pyr_kernel");
 }
@@ -549,7 +591,8 @@ int kv_summary_run(const void* k, const int64_t ks[4], const void* v, const int6
   SPRUCE_REQUIRE(g1 < ((int64_t)1 << 31) && g2 < ((int64_t)1 << 31), "too many workgroups");
   const int eb = dtype == SPRUCE_DTYPE_F32 ? 4 : 2;
   const bool vec = D % 64 == 0 && D <= 256 && ks[3] == 1 && vs[3] == 1 && ((uintptr_t)k % 16) == 0 &&
-                   ((uintptr_t)v % 16) == 0 && (ks[0] * eb) % 16 == 0 && (ks[1] * eb) % 16 == 0 &&
+                   ((uintptr_t)v % 16) == 0 && ((uintptr_t)keys % 16) == 0 && ((uintptr_t)values % 16) == 0 &&
+                   (ks[0] * eb) % 16 == 0 && (ks[1] * eb) % 16 == 0 &&
                    (ks[2] * eb) % 16 == 0 && (vs[0] * eb) % 16 == 0 && (vs[1] * eb) % 16 == 0 &&
                    (vs[2] * eb) % 16 == 0;
   if (!vec) {
