@@ -395,6 +395,17 @@ int spruce_teacher_targets(const float* mass, int64_t B, int64_t Hq, int64_t Hkv
                            void* stream);
 
 /*
+ * The first half of spruce_teacher_targets alone: group_mass = the mean of
+ * mass over each KV group's query heads, zero above the diagonal, and
+ * row_mass its row sum, without normalisation (load_teacher with
+ * defer_normalization=True, selector/targets.py:104-113).
+ *   mass [B, Hq, Qb, Kb] -> group_mass [B, Hkv, Qb, Kb], row_mass [B, Hkv, Qb];
+ *   all contiguous; Kb <= 8192.
+ */
+int spruce_teacher_group_mass(const float* mass, int64_t B, int64_t Hq, int64_t Hkv, int64_t Qb, int64_t Kb,
+                              float* group_mass, float* row_mass, void* stream);
+
+/*
  * Selector prototype features in the model dtype.  Replaces _proto_pool_seq
  * (teacher/chunked_extract.py:27-72) applied to _group_avg_tokens (:75-80):
  * x [B, H, L, D] (strided, element strides xs) is averaged over the H/G heads

@@ -30,6 +30,8 @@ imports it.
   teacher_targets  selector/targets.py:104-121 (group mean, causal mask, row
                    normalisation with eps) plus the top-k target blocks of
                    selector/loss.py:34-46 (target.topk).
+  group_mass       the first half of teacher_targets alone (the mass that
+                   load_teacher keeps with defer_normalization).
 """
 import math
 
@@ -106,6 +108,17 @@ def chunked_pool(query, key, scaling, block=BLOCK, head_chunk=2, heads=None):
             p = p.view(b, len(hs), r1 - r0, kb_up, block).sum(dim=-1)
             pooled[:, hs, I, :kb_up] = p.sum(dim=2)
     return pooled
+
+
+@torch.no_grad()
+def group_mass(mass, num_kv_heads):
+    """mass [b, H, qb, kb] -> the KV-group mean with the causal mask
+    [b, G, qb, kb] (selector/targets.py:104-108, the mass load_teacher keeps
+    with defer_normalization)."""
+    b, H, qb, kb = mass.shape
+    m = mass.view(b, num_kv_heads, H // num_kv_heads, qb, kb).mean(dim=2)
+    cmask = torch.arange(kb)[None, :] <= torch.arange(qb)[:, None]
+    return m * cmask
 
 
 @torch.no_grad()

@@ -309,6 +309,9 @@ __device__ __forceinline__ uint32_t target_key(float f) {
 // causal mask, row normalisation, then the k largest targets (descending,
 // ties to the lower block index; -1 padding for short causal rows).
 constexpr int kTgtMaxKb = 8192;
+// NORM = false: only the group mean with the causal mask (into target) and its
+// row sum, for callers that normalise later.
+template <bool NORM>
 __global__ __launch_bounds__(256) void teacher_targets_kernel(const float* __restrict__ mass, int Hq, int Hkv,
                                                               int Qb, int Kb, int k, float eps,
                                                               float* __restrict__ target, float* __restrict__ row_mass,
@@ -343,8 +346,13 @@ __global__ __launch_bounds__(256) void teacher_targets_kernel(const float* __res
     __syncthreads();
   }
   const float rs = red[0];
-  const float den = rs > eps ? rs : eps;
   float* trow = target + (int64_t)row * Kb;
+  if constexpr (!NORM) {
+    for (int j = tid; j < Kb; j += 256) trow[j] = vals[j];
+    if (tid == 0) row_mass[row] = rs;
+    return;
+  }
+  const float den = rs > eps ? rs : eps;
   for (int j = tid; j < Kb; j += 256) {
     const float t = vals[j] / den;
     trow[j] = t;
@@ -571,7 +579,19 @@ extern "C" int spruce_teacher_targets(const float* mass, int64_t B, int64_t Hq, 
   SPRUCE_REQUIRE(k >= 1 && k <= 64, "k must be in [1, 64], got %lld", (long long)k);
   SPRUCE_REQUIRE(Kb <= kTgtMaxKb, "at most %d key blocks per row are supported", kTgtMaxKb);
   SPRUCE_REQUIRE(B * Hkv * Qb < ((int64_t)1 << 31), "too many rows");
-  hipLaunchKernelGGL(teacher_targets_kernel, dim3((unsigned)(B * Hkv * Qb)), dim3(256), 0, (hipStream_t)stream, mass,
-                     (int)Hq, (int)Hkv, (int)Qb, (int)Kb, (int)k, eps, target, row_mass, topk);
+  hipLaunchKernelGGL(teacher_targets_kernel<true>, dim3((unsigned)(B * Hkv * Qb)), dim3(256), 0, (hipStream_t)stream,
+                     mass, (int)Hq, (int)Hkv, (int)Qb, (int)Kb, (int)k, eps, target, row_mass, topk);
+  return check_launch("teacher_targets_kernel");
+}
+
+extern "C" int spruce_teacher_group_mass(const float* mass, int64_t B, int64_t Hq, int64_t Hkv, int64_t Qb,
+                                         int64_t Kb, float* group_mass, float* row_mass, void* stream) {
+  SPRUCE_REQUIRE(mass && group_mass && row_mass, "mass, group_mass and row_mass must be non-null");
+  SPRUCE_REQUIRE(B >= 1 && Hkv >= 1 && Hq >= Hkv && Hq % Hkv == 0 && Qb >= 1 && Kb >= 1, "invalid shape");
+  SPRUCE_REQUIRE(Kb <= kTgtMaxKb, "at most %d key blocks per row are supported", kTgtMaxKb);
+  SPRUCE_REQUIRE(B * Hkv * Qb < ((int64_t)1 << 31), "too many rows");
+  hipLaunchKernelGGL(teacher_targets_kernel<false>, dim3((unsigned)(B * Hkv * Qb)), dim3(256), 0,
+                     (hipStream_t)stream, mass, (int)Hq, (int)Hkv, (int)Qb, (int)Kb, 0, 0.f, group_mass, row_mass,
+                     nullptr);
   return check_launch("teacher_targets_kernel");
 }

@@ -62,6 +62,7 @@ _SIGNATURES = {
     "spruce_teacher_schedule": [_i64, _i64, _i64, _i64, _i64, ctypes.c_size_t],
     "spruce_teacher_targets": [
         _p, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _p, _p, _p, _p],
+    "spruce_teacher_group_mass": [_p, _i64, _i64, _i64, _i64, _i64, _p, _p, _p],
     "spruce_pack_selected_ids": [_p, ctypes.c_int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "spruce_pack_selected_mask": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "spruce_proto_pool": [_p, _STRIDES, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _p],

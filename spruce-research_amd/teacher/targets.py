@@ -37,6 +37,30 @@ def teacher_targets(mass, num_kv_heads, k=8, eps=1e-9):
     return {"target": target, "row_mass": row_mass, "topk": topk, "cmask": cmask}
 
 
+@torch.no_grad()
+def teacher_group_mass(mass, num_kv_heads):
+    """mass ``[B, H, Qb, Kb]`` float32 -> (group mean with the causal mask
+    ``[B, G, Qb, Kb]``, its row sums ``[B, G, Qb]``): the unnormalised half of
+    :func:`teacher_targets` (selector/targets.py:104-113)."""
+    if not mass.is_cuda:
+        raise RuntimeError("teacher_group_mass (HIP) requires a GPU tensor")
+    if mass.dim() != 4 or mass.dtype != torch.float32:
+        raise ValueError("mass must be float32 [B, H, Qb, Kb]")
+    B, H, Qb, Kb = mass.shape
+    G = int(num_kv_heads)
+    if G < 1 or H % G:
+        raise ValueError(f"H={H} not divisible by G={G}")
+    mass = mass.contiguous()
+    out = torch.empty((B, G, Qb, Kb), device=mass.device, dtype=torch.float32)
+    row_mass = torch.empty((B, G, Qb), device=mass.device, dtype=torch.float32)
+    with torch.cuda.device(mass.device):
+        rc = spruce_hip.lib().spruce_teacher_group_mass(
+            spruce_hip.ptr(mass), B, H, G, Qb, Kb, spruce_hip.ptr(out), spruce_hip.ptr(row_mass),
+            spruce_hip.stream_of(mass))
+    spruce_hip.check(rc, "spruce_teacher_group_mass")
+    return out, row_mass
+
+
 def causal_block_mask(qb, kb, device=None):
     """Query block q may attend key block k iff k <= q (selector/targets.py:54-59)."""
     q = torch.arange(qb, device=device)[:, None]

@@ -88,6 +88,9 @@ def test_chunked_pool_and_targets_match_float64_oracle():
     et, er, etop = ot.targets(exp, 2, k=3)
     np.testing.assert_allclose(t.double().numpy(), et, atol=1e-6)
     np.testing.assert_allclose(r.double().numpy(), er, atol=1e-4)
+    gm = rc.group_mass(mass, 2)
+    np.testing.assert_allclose(gm.double().numpy(), er[..., None] * et, atol=1e-5)
+    assert torch.equal(gm / gm.sum(-1, keepdim=True).clamp_min(1e-9), t)
     part = rc.chunked_pool(q, k, 64 ** -0.5, heads=[5])
     assert torch.equal(part[:, 5], mass[:, 5]) and part[:, :5].abs().sum() == 0
 
