@@ -704,30 +704,33 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
   // l rescale); O^T += V^T P^T.
   f32x16_t sc0, sc1;
   uint4 pk[2][2];
-  // LDS fragment reads are interleaved with the MFMAs that consume them
-  // (kLookahead k-steps ahead, pinned by scheduling-group barriers), so the
-  // waves' LDS traffic overlaps their matrix-core work instead of running as
-  // a separate phase in which all waves of the workgroup contend for LDS.
+  // LDS fragment reads are interleaved with the MFMAs that consume them,
+  // kLookahead k-steps ahead, so the waves' LDS traffic overlaps their
+  // matrix-core work instead of running as a separate phase in which all
+  // waves of the workgroup contend for LDS.  The order is pinned by
+  // scheduling barriers in the S^T loop and scheduling-group barriers in the
+  // P.V loop; without the former the scheduler reused one register quad for
+  // every K fragment, one read in flight per MFMA.
   auto scores = [&](const uint16_t* Ks) {
     const uint16_t* kp = Ks + l32 * KSTR + 8 * hl;
     uint4 a0[KS], a1[KS];
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
+    auto rd = [&](int kk) {
       a0[kk] = *reinterpret_cast<const uint4*>(kp + 16 * kk);
       a1[kk] = *reinterpret_cast<const uint4*>(kp + 32 * KSTR + 16 * kk);
-    }
-    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * kLookahead, 0);
+    };
 #pragma unroll
-    for (int i = 0; i < KS - kLookahead; ++i) {
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2 * kLookahead, 0);
+    for (int kk = 0; kk < kLookahead; ++kk) rd(kk);
     f32x16_t s0 = f32x16_t{}, s1 = f32x16_t{};
+    // Scheduling barriers pin the order: the reads of step kk + kLookahead
+    // are issued before the MFMAs of step kk, so the fragments of three steps
+    // are live in distinct registers and each MFMA waits only for its own.
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
+      if (kk + kLookahead < KS) rd(kk + kLookahead);
+      __builtin_amdgcn_sched_barrier(0);
       s0 = mfma32x32x16<F16>(a0[kk], qf[kk], s0);
       s1 = mfma32x32x16<F16>(a1[kk], qf[kk], s1);
+      __builtin_amdgcn_sched_barrier(0);
     }
     sc0 = s0;
     sc1 = s1;
