@@ -33,7 +33,8 @@
 //   single pass (when its scratch fits, see kSinglePassScratchMax): online
 //     row reference point and denominator, and for every J the row's partial
 //     sum e_J = sum_j exp2(s_j - m_J) with its reference point m_J written to
-//     scratch (8 bytes per row and J); once the row is complete the wave
+//     scratch (8 bytes per row and J, staged in LDS and copied every kRing
+//     blocks); once the row is complete the wave
 //     reads them back and sums e_J * exp2(m_J - m) / l over its 32 rows in a
 //     fixed butterfly order.  QK^T runs once.
 //   two passes (longer sequences): pass 1 keeps only the row reference point
@@ -72,6 +73,10 @@ inline int64_t single_pass_scratch_bytes(int64_t B, int64_t Hq, int64_t Qb) {
 // kRescaleThreshold).
 constexpr float kMassCheckSum = 256.0f;
 
+// Key blocks whose per-row partials a wave stages in LDS before one copy to
+// the single-pass scratch.
+constexpr int kRing = 8;
+
 // PASS 1: row statistics; PASS 2: tile mass from them; PASS 3: single pass
 // with per-row partials in the workspace.
 template <int D, int WAVES, typename TIn, bool F16, int PASS>
@@ -86,6 +91,9 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
   constexpr int EB = TIn::bytes;
 
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * KTILE];
+  // Single pass: each wave stages its rows' (e_J, m_J) for kRing blocks here
+  // and copies them to the scratch in one go (see flush_ring).
+  __shared__ __attribute__((aligned(16))) float2 ring[PASS == 3 ? WAVES : 1][PASS == 3 ? kRing * 32 : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps per-wave addresses scalar
@@ -161,6 +169,24 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
     rowj = p.rowj + ((((int64_t)b * p.Hq + head) * 2 + half) * ((int64_t)p.Qb * (p.Qb + 1) / 2) +
                      (int64_t)qb * (qb + 1) / 2) * 32;
 
+  // Copies ring slots 0..n-1 (blocks J0..J0+n-1, J0 a multiple of kRing) to
+  // the scratch: 16 bytes per lane per store, kRing * 256 bytes contiguous.
+  // Staging through LDS keeps the global stores to one block in kRing: a
+  // store still in flight makes the next K staging wait for its write
+  // acknowledgement (loads and stores share the counter and may complete
+  // out of order), which per block cost about a tenth of the kernel time.
+  auto flush_ring = [&](int J0, int n) {
+    if constexpr (PASS == 3) {
+      const float4* src = reinterpret_cast<const float4*>(&ring[wave][0]);
+      float4* dst = reinterpret_cast<float4*>(rowj + (int64_t)J0 * 32);
+#pragma unroll
+      for (int i = 0; i < kRing * 16 / 64; ++i) {
+        const int f = lane + 64 * i;  // float4 index: block f / 16, rows 2(f % 16) and 2(f % 16) + 1
+        if (f < n * 16) dst[f] = src[f];
+      }
+    }
+  };
+
   // One block of the row: S^T = K Q^T (from the reference point), the
   // exponentials, the row-statistics update (PASS 1/3) and the partial
   // (PASS 3) or tile mass (PASS 2).  The diagonal block (last) is the only
@@ -223,7 +249,8 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
       l_run += ps;
       if (PASS == 3) {
         const float e = ps + __shfl_xor(ps, 32);
-        if (hl == 0) rowj[(int64_t)J * 32 + l32] = float2{e, m_use};
+        if (hl == 0) ring[PASS == 3 ? wave : 0][(J % kRing) * 32 + l32] = float2{e, m_use};
+        if (J % kRing == kRing - 1) flush_ring(J - (kRing - 1), kRing);
       }
     } else {
       float v = (qtok < p.T) ? ps * inv_l : 0.f;
@@ -254,6 +281,7 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
     }
   }
   if (PASS == 3 && active) {
+    if (qb % kRing != kRing - 1) flush_ring(qb - qb % kRing, qb % kRing + 1);
     const float lt = l_run + __shfl_xor(l_run, 32);
     const float inv = (qtok < p.T && lt > 0.f) ? 1.f / lt : 0.f;
     // The wave reads back only what it wrote, on the same CU: a
