@@ -108,6 +108,25 @@ __device__ __forceinline__ float group_avg1(const ProtoParams& p, int b, int h0,
   return round_to(s * p.inv_rep, p.dtype);
 }
 
+// Maximum of v over the 64 lanes, in every lane: prefix maxima within each
+// 16-lane row by DPP row shifts (lanes shifted in from outside the row keep
+// their own value), then row 0's and row 2's last lanes broadcast into rows
+// 1 and 3 and lane 31 into rows 2 and 3, so lane 63 holds the wave maximum.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  auto mx = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
+  v = mx(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, false));  // row_shr:1
+  v = mx(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, false));  // row_shr:2
+  v = mx(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, false));  // row_shr:4
+  v = mx(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, false));  // row_shr:8
+  v = mx(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false));  // row_bcast:15
+  v = mx(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false));  // row_bcast:31
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Token chunks per thread whose loads are issued together on the key side
+// (one head): a 64-token block of D = 128 is 4 chunks per thread.
+constexpr int kProtoBatchK = 4;
+
 // Token chunks whose loads are issued together in the 16-bit group average.
 // Measured at cfg3 (Q, 28/4 heads, 64K tokens): 0.129 ms with group_avg8,
 // 0.097 ms with 2, 0.098 ms with 1, 0.101 ms with 4.
@@ -172,6 +191,36 @@ __global__ __launch_bounds__(256) void proto_pool_kernel(ProtoParams p) {
         for (int j = 0; j < 8; ++j) tile[t][8 * c + j] = round_to(sum[j] * p.inv_rep, p.dtype);
       }
     }
+  } else if (vec && p.dtype != SPRUCE_DTYPE_F32 && p.rep == 1) {
+    // One head (the key side): the row is copied unchanged, so the raw
+    // 16-byte chunks of kProtoBatchK token chunks are all loaded first and
+    // then widened into the tile (one memory round trip for a 64 x 128 block).
+    const int dch = p.D >> 3;
+    const bool f16 = p.dtype == SPRUCE_DTYPE_F16;
+    for (int e0 = tid; e0 < n * dch; e0 += 256 * kProtoBatchK) {
+      uint4 raw[kProtoBatchK];
+#pragma unroll
+      for (int k = 0; k < kProtoBatchK; ++k) {
+        const int e = e0 + 256 * k;
+        if (e < n * dch) {
+          const int t = e / dch, c = e - (e / dch) * dch;
+          raw[k] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.x) + (int64_t)b * p.xs[0] +
+                                                   (int64_t)h0 * p.xs[1] + (int64_t)(t0 + t) * p.xs[2] + 8 * c);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kProtoBatchK; ++k) {
+        const int e = e0 + 256 * k;
+        if (e >= n * dch) break;
+        const int t = e / dch, c = e - (e / dch) * dch;
+        const uint32_t w[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          tile[t][8 * c + 2 * i] = f16 ? unpack1<true>(w[i] & 0xffffu) : unpack1<false>(w[i] & 0xffffu);
+          tile[t][8 * c + 2 * i + 1] = f16 ? unpack1<true>(w[i] >> 16) : unpack1<false>(w[i] >> 16);
+        }
+      }
+    }
   } else if (vec) {
     const int dch = p.D >> 3;
     for (int e = tid; e < n * dch; e += 256) {
@@ -230,14 +279,13 @@ __global__ __launch_bounds__(256) void proto_pool_kernel(ProtoParams p) {
     const uint32_t okey = dist != dist ? 0xffffffffu                    // any NaN ranks above +inf
                                        : ((u & 0x80000000u) ? ~u : (u | 0x80000000u));
     bool taken = !in_block;
+    // Each round: the largest order key among the rows not yet taken (every
+    // such key is at least 0x007fffff, taken rows count as 0), then the
+    // lowest row holding it (ties to the lower row).
     for (int j = 0; j < k; ++j) {
-      uint64_t key = taken ? 0ull : (((uint64_t)okey << 32) | (uint32_t)(63 - tid));
-#pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) {
-        const uint64_t o = __shfl_xor(key, m, 64);
-        key = o > key ? o : key;
-      }
-      const int best = 63 - (int)(key & 63u);
+      const uint32_t key = taken ? 0u : okey;
+      const uint32_t top = wave_max_u32(key);
+      const int best = (int)__builtin_ctzll(__ballot(key == top));
       if (tid == best) taken = true;
       if (tid == 0) pick[j] = best;
     }
