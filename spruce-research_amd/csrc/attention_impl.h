@@ -775,7 +775,7 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     for (int r = 2; r < 16; ++r) mx = fmaxf(mx, s0[r]);
 #pragma unroll
     for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s1[r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = half_max(mx);
     const float cand = mx * p.cs;
     if (__ballot(cand > m_use + kRescaleThreshold) != 0) {
       const float m_new = fmaxf(m_use, cand);
@@ -1009,7 +1009,7 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     static_assert(WAVES * 32 * OSTR <= 2 * BUF, "output staging must fit the K/V tiles");
     __syncthreads();
     if (!active) return;
-    const float lt = l_run + __shfl_xor(l_run, 32);
+    const float lt = half_sum(l_run);
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
     uint16_t* ot = smem + wave * 32 * OSTR;
 #pragma unroll
@@ -1042,7 +1042,7 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     return;
   }
   if (!active) return;
-  const float lt = l_run + __shfl_xor(l_run, 32);
+  const float lt = half_sum(l_run);
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
   const int64_t ors = p.os[2] * EB;
   int nq = p.T - q0;

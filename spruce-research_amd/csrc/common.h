@@ -77,6 +77,31 @@ __device__ __forceinline__ f32x16_t mfma32x32x16(uint4 a, uint4 b, f32x16_t c) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// x of lane l combined with x of lane l ^ 32, without the LDS round trip of a
+// ds_bpermute: v_permlane32_swap(a, b) exchanges the upper half of a with the
+// lower half of b, so with a = b = x every lane holds x[l] in one result and
+// x[l ^ 32] in the other.  Both combinations are commutative, so the result
+// equals x + __shfl_xor(x, 32) (resp. fmaxf) bit for bit.  (Each result is
+// read into an unsigned before any bit cast: a bit cast of the vector element
+// itself compiles to a read of element 0.)
+__device__ __forceinline__ void half_swap(float x, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                  false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  a = __builtin_bit_cast(float, r0);
+  b = __builtin_bit_cast(float, r1);
+}
+__device__ __forceinline__ float half_sum(float x) {
+  float a, b;
+  half_swap(x, a, b);
+  return a + b;
+}
+__device__ __forceinline__ float half_max(float x) {
+  float a, b;
+  half_swap(x, a, b);
+  return fmaxf(a, b);
+}
+
 // Loads 8 consecutive elements of type TIn at p and returns them as eight
 // 16-bit MFMA inputs (bf16 bits, or f16 bits when F16).  Out-of-range rows are
 // handled by the caller (valid == false returns zeros).

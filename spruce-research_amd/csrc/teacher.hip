@@ -235,7 +235,7 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
         for (int r = 2; r < 16; ++r) mx = fmaxf(mx, s0[r]);
 #pragma unroll
         for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s1[r]);
-        mx = fmaf(fmaxf(mx, __shfl_xor(mx, 32)), cs, nm);  // relative to m_use
+        mx = fmaf(half_max(mx), cs, nm);  // relative to m_use
         const float delta = (J == 0 || mx > kRescaleThreshold) ? mx : 0.f;
         if (__ballot(delta != 0.f) != 0) {
           m_use += delta;
@@ -248,7 +248,7 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
       }
       l_run += ps;
       if (PASS == 3) {
-        const float e = ps + __shfl_xor(ps, 32);
+        const float e = half_sum(ps);
         if (hl == 0) ring[PASS == 3 ? wave : 0][(J % kRing) * 32 + l32] = float2{e, m_use};
         if (J % kRing == kRing - 1) flush_ring(J - (kRing - 1), kRing);
       }
@@ -274,7 +274,7 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
   }
   if (active) step(std::true_type{}, qb, buf);
   if (PASS == 1 && active) {
-    const float lt = l_run + __shfl_xor(l_run, 32);
+    const float lt = half_sum(l_run);
     if (hl == 0 && qtok < p.T) {
       stat[0] = m_use;
       stat[1] = lt;
@@ -282,7 +282,7 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
   }
   if (PASS == 3 && active) {
     if (qb % kRing != kRing - 1) flush_ring(qb - qb % kRing, qb % kRing + 1);
-    const float lt = l_run + __shfl_xor(l_run, 32);
+    const float lt = half_sum(l_run);
     const float inv = (qtok < p.T && lt > 0.f) ? 1.f / lt : 0.f;
     // The wave reads back only what it wrote, on the same CU: a
     // workgroup-scope fence (wait for the stores) orders them before the
