@@ -406,15 +406,14 @@ __device__ void capture_key_prototypes(const uint16_t* Ks, float* scratch, int n
     // Order key: larger distance first, any NaN above +inf, then lower row.
     const uint32_t u = __builtin_bit_cast(uint32_t, dist);
     const uint32_t okey = dist != dist ? 0xffffffffu : ((u & 0x80000000u) ? ~u : (u | 0x80000000u));
+    // Each round: the largest key among the rows not yet taken (every such
+    // key is at least 0x007fffff, taken rows count as 0), then the lowest row
+    // holding it.
     bool taken = false;
     for (int j = 0; j < k; ++j) {
-      uint64_t key = taken ? 0ull : (((uint64_t)okey << 32) | (uint32_t)(63 - tid));
-#pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) {
-        const uint64_t o = __shfl_xor(key, m, 64);
-        key = o > key ? o : key;
-      }
-      const int best = 63 - (int)(key & 63u);
+      const uint32_t key = taken ? 0u : okey;
+      const uint32_t top = wave_max_u32(key);
+      const int best = (int)__builtin_ctzll(__ballot(key == top));
       if (tid == best) taken = true;
       if (tid == 0) pick[j] = best;
     }

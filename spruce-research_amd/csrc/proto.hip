@@ -108,21 +108,6 @@ __device__ __forceinline__ float group_avg1(const ProtoParams& p, int b, int h0,
   return round_to(s * p.inv_rep, p.dtype);
 }
 
-// Maximum of v over the 64 lanes, in every lane: prefix maxima within each
-// 16-lane row by DPP row shifts (lanes shifted in from outside the row keep
-// their own value), then row 0's and row 2's last lanes broadcast into rows
-// 1 and 3 and lane 31 into rows 2 and 3, so lane 63 holds the wave maximum.
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-  auto mx = [](uint32_t a, uint32_t b) { return a > b ? a : b; };
-  v = mx(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, false));  // row_shr:1
-  v = mx(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, false));  // row_shr:2
-  v = mx(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, false));  // row_shr:4
-  v = mx(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, false));  // row_shr:8
-  v = mx(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false));  // row_bcast:15
-  v = mx(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false));  // row_bcast:31
-  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
-}
-
 // Token chunks per thread whose loads are issued together on the key side
 // (one head): a 64-token block of D = 128 is 4 chunks per thread.
 constexpr int kProtoBatchK = 4;
