@@ -977,14 +977,60 @@ __global__ __launch_bounds__(256) void causal_topk_wave_kernel(const float* __re
   // keys are then the top k (the k-th largest is >= it and the (k+1)-th is
   // below), and the compaction below takes exactly them, as it would with the
   // k-th largest key itself as T.
+  //
+  // First a cheap bound: t0 = the k-th largest of the 64 lane maxima (k <=
+  // 64), so at least k keys are >= t0 and the k-th largest key T is >= t0.
+  // When at most 64 keys are >= t0 they are compacted into one slot per lane
+  // and T is searched among them: for every candidate value >= t0 their count
+  // equals the count over all keys, and below t0 both are >= k, so the search
+  // ends at the same T (the early exit is taken only at or above t0).
+  // Otherwise the search runs over all 16 slots.
   uint32_t T = 0;
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t cand = T | (1u << bit);
-    int cnt = 0;
+  __shared__ uint32_t cands[4][64];
+  int nc = kWaveTopkKb + 1;
+  uint32_t t0 = 0;
+  if (k <= 64) {
+    uint32_t lmax = key[0];
 #pragma unroll
-    for (int s = 0; s < kWaveTopkPer; ++s) cnt += __popcll(__ballot(key[s] >= cand));
-    if (cnt >= k) T = cand;
-    if (cnt == k) break;
+    for (int s = 1; s < kWaveTopkPer; ++s) lmax = key[s] > lmax ? key[s] : lmax;
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t cand = t0 | (1u << bit);
+      if (__popcll(__ballot(lmax >= cand)) >= k) t0 = cand;
+    }
+    nc = 0;
+#pragma unroll
+    for (int s = 0; s < kWaveTopkPer; ++s) nc += __popcll(__ballot(key[s] >= t0));
+  }
+  if (nc <= 64) {
+    uint32_t* cw = cands[threadIdx.x >> 6];
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    int base = 0;
+#pragma unroll
+    for (int s = 0; s < kWaveTopkPer; ++s) {
+      const bool c = key[s] >= t0;
+      const uint64_t b = __ballot(c);
+      if (c) cw[base + __popcll(b & below)] = key[s];
+      base += __popcll(b);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint32_t ck = lane < nc ? cw[lane] : 0u;
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t cand = T | (1u << bit);
+      const int cnt = __popcll(__ballot(ck >= cand));
+      if (cnt >= k) T = cand;
+      if (cnt == k && cand >= t0) break;
+    }
+  } else {
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t cand = T | (1u << bit);
+      int cnt = 0;
+#pragma unroll
+      for (int s = 0; s < kWaveTopkPer; ++s) cnt += __popcll(__ballot(key[s] >= cand));
+      if (cnt >= k) T = cand;
+      if (cnt == k) break;
+    }
   }
   int gt = 0;
 #pragma unroll

@@ -172,6 +172,23 @@ def test_topk_search_boundaries():
     assert np.array_equal(_np(got), osel.topk(s.numpy(), 32))
 
 
+@pytest.mark.parametrize("k", [1, 8, 32, 64, 65])
+def test_topk_candidate_search_and_its_fallback(k):
+    # The top-k search first bounds the k-th key by the k-th largest lane
+    # maximum and searches among the (at most 64) keys above that bound;
+    # rows with more than 64 such keys (heavy ties, few distinct values) and
+    # k > 64 take the full search.  Both must give the oracle's indices.
+    gen = torch.Generator().manual_seed(23)
+    s = torch.randn(4, 1024, 1024, generator=gen)            # distinct keys: the candidate search
+    s[1] = torch.randint(0, 3, (1024, 1024), generator=gen).float()   # three values: the fallback
+    s[2, :, :] = 0.25                                         # one value everywhere
+    s[3] = torch.randint(0, 40, (1024, 1024), generator=gen).float() * 0.5
+    s[3, 600, :601] = torch.arange(601, dtype=torch.float32).flip(0)  # strictly decreasing row
+    s[3, 601, 7::64] = 50.0                                   # the top keys all in one lane
+    got = causal_topk_blocks(s.to(DEV), k)
+    assert np.array_equal(_np(got), osel.topk(s.numpy(), k))
+
+
 def test_flat_gate_matches_reference_bruteforce():
     # Reference tests/test_gate_maxsim.py:22-33 on the HIP scorer.
     torch.manual_seed(0)
