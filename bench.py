@@ -198,7 +198,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU's share of the layer; multi-GPU runs are not part of "
-              "this build (the layer shards by KV head with no exchange, see DESIGN.md)",
+              "this build (the layer shards by KV head, each GPU owning whole KV heads, with no exchange)",
               file=sys.stderr)
         sys.exit(2)
 
