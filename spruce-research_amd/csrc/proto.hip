@@ -18,8 +18,12 @@
 //   distance       sum_d (a_d - m_d)^2 in float32, dims in order.
 //   top-k          descending distance, ties to the lower row, NaN largest.
 // rnd() rounds to the model dtype (nearest even); float32 input is exact.
-// One workgroup per (batch, KV group, block); the block tile is held in LDS as
-// float.  HBM-bound: every input element is read once.
+// One workgroup per (batch, KV group, block); the block tile is held in LDS,
+// as float, or for 16-bit single-head input (the key side) as the raw 16-bit
+// words, which halves the workgroup's LDS.  HBM-bound: every input element is
+// read once.
+#include <type_traits>
+
 #include "common.h"
 
 namespace spruce {
@@ -116,12 +120,32 @@ constexpr int kProtoBatchK = 4;
 // Measured at cfg3 (Q, 28/4 heads, 64K tokens): 0.129 ms with group_avg8,
 // 0.097 ms with 2, 0.098 ms with 1, 0.101 ms with 4.
 constexpr int kProtoBatch = 2;
+// Load paths: kProtoAny (every dtype and layout), kProtoGroup16 (16-bit,
+// contiguous rows, 2..8 heads per group), kProtoOne16 (16-bit, contiguous
+// rows, one head: the only path with a 16-bit tile).  F16: the 16-bit input
+// is f16 (else bf16).  At the key side the 16-bit tile (7 instead of 4
+// workgroups per CU) takes cfg3's K 32 -> 26 us; at the group-average path,
+// bound by its 7 heads' loads, a 16-bit tile measured the same as this float
+// one (91.5 vs 91.2 us).
+constexpr int kProtoAny = 0, kProtoGroup16 = 1, kProtoOne16 = 2;
+
+template <int PATH, bool F16>
 __global__ __launch_bounds__(256) void proto_pool_kernel(ProtoParams p) {
-  // Rows padded to D + 4 floats: 16-byte aligned for the float4 distance
-  // reads and spread over the banks.
-  __shared__ __attribute__((aligned(16))) float tile[kProtoMaxBlock][kProtoMaxD + 4];
+  constexpr bool T16 = PATH == kProtoOne16;
+  using TileT = std::conditional_t<T16, uint16_t, float>;
+  // Rows padded by 16 bytes: 16-byte aligned for the vector distance reads
+  // and spread over the banks.
+  constexpr int TSTR = kProtoMaxD + (T16 ? 8 : 4);
+  __shared__ __attribute__((aligned(16))) TileT tile[kProtoMaxBlock][TSTR];
   __shared__ __attribute__((aligned(16))) float mean[kProtoMaxD];
   __shared__ int pick[kProtoMaxP];
+  auto tget = [&](int t, int d) -> float {
+    if constexpr (T16) {
+      return unpack1<F16>(tile[t][d]);
+    } else {
+      return tile[t][d];
+    }
+  };
   const int tid = threadIdx.x;
   const int i = blockIdx.x % p.nb;
   const int bg = blockIdx.x / p.nb;
@@ -132,32 +156,35 @@ __global__ __launch_bounds__(256) void proto_pool_kernel(ProtoParams p) {
   const int h0 = g * p.rep;
   const bool vec = (p.D & 7) == 0 && p.xs[3] == 1;
 
-  if (vec && p.dtype != SPRUCE_DTYPE_F32 && p.rep > 1 && p.rep <= 8) {
+  if constexpr (PATH == kProtoGroup16) {
     // 16-bit inputs: the raw 16-byte loads of kProtoBatch token chunks (all
     // their heads) are issued before the first add and widened only when
     // added, so a 64-token block of D = 128 costs 4 / kProtoBatch memory
     // round trips; the sums are the same ordered sequence as group_avg8.
+    // The loads are unconditional, so they issue back to back: heads past
+    // rep re-read head h0's chunk and chunks past the block re-read its last
+    // one (both in range, neither added or stored).
     const int dch = p.D >> 3;
-    const bool f16 = p.dtype == SPRUCE_DTYPE_F16;
-    for (int e0 = tid; e0 < n * dch; e0 += 256 * kProtoBatch) {
+    const int ne = n * dch;  // 16-byte chunks per head of the block, >= 1
+    const uint16_t* xb = static_cast<const uint16_t*>(p.x) + (int64_t)b * p.xs[0];
+    for (int e0 = tid; e0 < ne; e0 += 256 * kProtoBatch) {
       uint4 raw[kProtoBatch][8];
 #pragma unroll
       for (int k = 0; k < kProtoBatch; ++k) {
-        const int e = e0 + 256 * k;
-        if (e < n * dch) {
-          const int t = e / dch, c = e - (e / dch) * dch;
-          const int64_t base = (int64_t)b * p.xs[0] + (int64_t)(t0 + t) * p.xs[2] + 8 * c;
+        const int e = min(e0 + 256 * k, ne - 1);
+        const int t = e / dch, c = e - (e / dch) * dch;
+        const uint16_t* row = xb + (int64_t)(t0 + t) * p.xs[2] + 8 * c;
 #pragma unroll
-          for (int h = 0; h < 8; ++h)
-            if (h < p.rep)
-              raw[k][h] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.x) + base +
-                                                          (int64_t)(h0 + h) * p.xs[1]);
-        }
+        for (int h = 0; h < 8; ++h)
+          raw[k][h] = *reinterpret_cast<const uint4*>(row + (int64_t)(h0 + (h < p.rep ? h : 0)) * p.xs[1]);
       }
+      // Keep every load ahead of the first add (the scheduler otherwise sinks
+      // the second chunk's loads to their uses, one round trip each).
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int k = 0; k < kProtoBatch; ++k) {
         const int e = e0 + 256 * k;
-        if (e >= n * dch) break;
+        if (e >= ne) break;
         const int t = e / dch, c = e - (e / dch) * dch;
         float sum[8];
 #pragma unroll
@@ -166,8 +193,8 @@ __global__ __launch_bounds__(256) void proto_pool_kernel(ProtoParams p) {
           const uint32_t w[4] = {raw[k][h].x, raw[k][h].y, raw[k][h].z, raw[k][h].w};
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float lo = f16 ? unpack1<true>(w[i] & 0xffffu) : unpack1<false>(w[i] & 0xffffu);
-            const float hi = f16 ? unpack1<true>(w[i] >> 16) : unpack1<false>(w[i] >> 16);
+            const float lo = unpack1<F16>(w[i] & 0xffffu);
+            const float hi = unpack1<F16>(w[i] >> 16);
             sum[2 * i] = h == 0 ? 0.0f + lo : sum[2 * i] + lo;
             sum[2 * i + 1] = h == 0 ? 0.0f + hi : sum[2 * i + 1] + hi;
           }
@@ -176,33 +203,29 @@ __global__ __launch_bounds__(256) void proto_pool_kernel(ProtoParams p) {
         for (int j = 0; j < 8; ++j) tile[t][8 * c + j] = round_to(sum[j] * p.inv_rep, p.dtype);
       }
     }
-  } else if (vec && p.dtype != SPRUCE_DTYPE_F32 && p.rep == 1) {
+  } else if constexpr (PATH == kProtoOne16) {
     // One head (the key side): the row is copied unchanged, so the raw
     // 16-byte chunks of kProtoBatchK token chunks are all loaded first and
-    // then widened into the tile (one memory round trip for a 64 x 128 block).
+    // then stored into the tile as they are (one memory round trip for a
+    // 64 x 128 block).
     const int dch = p.D >> 3;
-    const bool f16 = p.dtype == SPRUCE_DTYPE_F16;
-    for (int e0 = tid; e0 < n * dch; e0 += 256 * kProtoBatchK) {
+    const int ne = n * dch;  // 16-byte chunks of the block, >= 1
+    const uint16_t* xb = static_cast<const uint16_t*>(p.x) + (int64_t)b * p.xs[0] + (int64_t)h0 * p.xs[1];
+    for (int e0 = tid; e0 < ne; e0 += 256 * kProtoBatchK) {
+      // Chunks past the block load the last one again (in range; not stored).
       uint4 raw[kProtoBatchK];
 #pragma unroll
       for (int k = 0; k < kProtoBatchK; ++k) {
-        const int e = e0 + 256 * k;
-        if (e < n * dch) {
-          const int t = e / dch, c = e - (e / dch) * dch;
-          raw[k] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.x) + (int64_t)b * p.xs[0] +
-                                                   (int64_t)h0 * p.xs[1] + (int64_t)(t0 + t) * p.xs[2] + 8 * c);
-        }
+        const int e = min(e0 + 256 * k, ne - 1);
+        const int t = e / dch, c = e - (e / dch) * dch;
+        raw[k] = *reinterpret_cast<const uint4*>(xb + (int64_t)(t0 + t) * p.xs[2] + 8 * c);
       }
 #pragma unroll
       for (int k = 0; k < kProtoBatchK; ++k) {
         const int e = e0 + 256 * k;
-        if (e >= n * dch) break;
-        const int t = e / dch, c = e - (e / dch) * dch;
-        const uint32_t w[4] = {raw[k].x, raw[k].y, raw[k].z, raw[k].w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          tile[t][8 * c + 2 * i] = f16 ? unpack1<true>(w[i] & 0xffffu) : unpack1<false>(w[i] & 0xffffu);
-          tile[t][8 * c + 2 * i + 1] = f16 ? unpack1<true>(w[i] >> 16) : unpack1<false>(w[i] >> 16);
+        if (e < ne) {
+          const int t = e / dch, c = e - (e / dch) * dch;
+          *reinterpret_cast<uint4*>(&tile[t][8 * c]) = raw[k];
         }
       }
     }
@@ -226,7 +249,7 @@ __global__ __launch_bounds__(256) void proto_pool_kernel(ProtoParams p) {
   if (tid < p.D) {
     float s = 0.0f;
 #pragma unroll 8
-    for (int t = 0; t < n; ++t) s = s + tile[t][tid];
+    for (int t = 0; t < n; ++t) s = s + tget(t, tid);
     mean[tid] = round_to(round_to(s, p.dtype) / (float)n, p.dtype);
   }
   __syncthreads();
@@ -240,7 +263,14 @@ __global__ __launch_bounds__(256) void proto_pool_kernel(ProtoParams p) {
       if ((p.D & 3) == 0) {
 #pragma unroll 8
         for (int d = 0; d < p.D; d += 4) {
-          const float4 x = *reinterpret_cast<const float4*>(&tile[tid][d]);
+          float4 x;
+          if constexpr (T16) {
+            const uint2 w = *reinterpret_cast<const uint2*>(&tile[tid][d]);
+            x = float4{unpack1<F16>(w.x & 0xffffu), unpack1<F16>(w.x >> 16), unpack1<F16>(w.y & 0xffffu),
+                       unpack1<F16>(w.y >> 16)};
+          } else {
+            x = *reinterpret_cast<const float4*>(&tile[tid][d]);
+          }
           const float4 m = *reinterpret_cast<const float4*>(&mean[d]);
           float diff = x.x - m.x;
           s = s + diff * diff;
@@ -253,7 +283,7 @@ __global__ __launch_bounds__(256) void proto_pool_kernel(ProtoParams p) {
         }
       } else {
         for (int d = 0; d < p.D; ++d) {
-          const float diff = tile[tid][d] - mean[d];
+          const float diff = tget(tid, d) - mean[d];
           s = s + diff * diff;
         }
       }
@@ -283,7 +313,7 @@ __global__ __launch_bounds__(256) void proto_pool_kernel(ProtoParams p) {
     float v = mean[d];
     if (pr >= 1 && pr <= k) {
       const int row = pick[pr - 1];
-      if (row < n) v = tile[row][d];
+      if (row < n) v = tget(row, d);
     }
     store1(p.out, obase + e, p.dtype, v);
   }
@@ -361,7 +391,17 @@ extern "C" int spruce_proto_pool(const void* x, const int64_t xs[4], int64_t B, 
   p.nb = (int)((L + block - 1) / block);
   const int64_t grid = B * G * (int64_t)p.nb;
   SPRUCE_REQUIRE(grid < ((int64_t)1 << 31), "too many blocks");
-  hipLaunchKernelGGL(proto_pool_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, p);
+  const bool vec16 = (D & 7) == 0 && xs[3] == 1 && dtype != SPRUCE_DTYPE_F32;
+  const bool f16 = dtype == SPRUCE_DTYPE_F16;
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, p);
+  };
+  if (vec16 && p.rep == 1)
+    f16 ? launch(proto_pool_kernel<kProtoOne16, true>) : launch(proto_pool_kernel<kProtoOne16, false>);
+  else if (vec16 && p.rep <= 8)
+    f16 ? launch(proto_pool_kernel<kProtoGroup16, true>) : launch(proto_pool_kernel<kProtoGroup16, false>);
+  else
+    launch(proto_pool_kernel<kProtoAny, false>);
   return check_launch("proto_pool_kernel");
 }
 
