@@ -60,6 +60,8 @@ def test_reference_known_answers():
     (torch.float16, 1, 2, 1, 100, 16, 8, 12, "bhtd"),     # block 8, P > block + 1
     (torch.bfloat16, 1, 16, 2, 190, 128, 64, 8, "bhtd"),  # 8 heads per group, ragged last block
     (torch.float16, 2, 6, 2, 129, 96, 64, 8, "bthd"),     # 3 heads per group, 12 chunks per token
+    (torch.float16, 1, 4, 4, 333, 128, 64, 8, "bthd"),    # one head per group (16-bit tile), strided rows, ragged block
+    (torch.bfloat16, 1, 3, 3, 200, 64, 32, 8, "bhtd"),    # one head per group, 32-token blocks, ragged block
 ])
 def test_proto_pool_matches_oracle(dtype, B, H, G, L, d, block, P, layout):
     g = torch.Generator().manual_seed(L + H)
