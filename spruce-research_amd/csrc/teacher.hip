@@ -485,6 +485,138 @@ __global__ __launch_bounds__(256) void teacher_targets_kernel(const float* __res
   }
 }
 
+// Rows of at most 256 key blocks: one wavefront per row, entries j = lane +
+// 64 s (s < 4) in registers, no LDS staging of the row and no workgroup
+// barrier.  Results are those of teacher_targets_kernel bit for bit: the row
+// sum follows its 256-entry reduction tree (entries j and j + 128, then j and
+// j + 64, inside each lane; then lanes l and l + s for s = 32 .. 1), and the
+// top-k takes the same entries (every key above the m-th largest key T, then
+// the lowest-index keys equal to T) in the same order.
+constexpr int kTgtWaveKb = 256;
+
+template <bool NORM>
+__global__ __launch_bounds__(256) void teacher_targets_wave_kernel(const float* __restrict__ mass, int Hq, int Hkv,
+                                                                   int Qb, int Kb, int k, float eps, int rows,
+                                                                   float* __restrict__ target,
+                                                                   float* __restrict__ row_mass,
+                                                                   int32_t* __restrict__ topk) {
+  __shared__ int sel_idx[4][64];
+  __shared__ uint32_t sel_key[4][64];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int row = blockIdx.x * 4 + w;
+  if (row >= rows) return;  // uniform per wave; the kernel has no workgroup barrier
+  const int i = row % Qb;
+  const int bg = row / Qb;
+  const int g = bg % Hkv, b = bg / Hkv;
+  const int G = Hq / Hkv;
+  const int n = i + 1 < Kb ? i + 1 : Kb;
+  const int64_t hs = (int64_t)Qb * Kb;
+  const float* mrow = mass + ((((int64_t)b * Hq + g * G) * Qb) + i) * Kb;
+
+  // Group mean; every load is issued before the first add (entries past the
+  // causal range and heads past G re-read an entry in range, not added).
+  float v[4];
+  if (G <= 8) {
+    float x[4][8];
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      const int j = lane + 64 * s4;
+      const int jc = j < n ? j : n - 1;
+#pragma unroll
+      for (int h = 0; h < 8; ++h) x[s4][h] = mrow[(h < G ? h : 0) * hs + jc];
+    }
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      float a = 0.f;
+#pragma unroll
+      for (int h = 0; h < 8; ++h)
+        if (h < G) a += x[s4][h];
+      v[s4] = lane + 64 * s4 < n ? a / (float)G : 0.f;
+    }
+  } else {
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      const int j = lane + 64 * s4;
+      float a = 0.f;
+      if (j < n) {
+        for (int h = 0; h < G; ++h) a += mrow[h * hs + j];
+        a = a / (float)G;
+      }
+      v[s4] = a;
+    }
+  }
+  // Row sum in the workgroup kernel's tree order.
+  float x = ((0.f + v[0]) + (0.f + v[2])) + ((0.f + v[1]) + (0.f + v[3]));
+#pragma unroll
+  for (int st = 32; st >= 1; st >>= 1) x = x + __shfl_down(x, st);
+  const float rs = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
+  float* trow = target + (int64_t)row * Kb;
+  if (lane == 0) row_mass[row] = rs;
+  if constexpr (!NORM) {
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4)
+      if (lane + 64 * s4 < Kb) trow[lane + 64 * s4] = v[s4];
+    return;
+  }
+  const float den = rs > eps ? rs : eps;
+  uint32_t key[4];
+  bool ok[4];
+#pragma unroll
+  for (int s4 = 0; s4 < 4; ++s4) {
+    const int j = lane + 64 * s4;
+    const float t = v[s4] / den;
+    if (j < Kb) trow[j] = t;
+    ok[s4] = j < n;
+    key[s4] = target_key(t);
+  }
+  // T: the largest key with at least m keys at or above it (the m-th largest).
+  const int m = n < k ? n : k;
+  uint32_t T = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t c = T | (1u << bit);
+    int cnt = 0;
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) cnt += __popcll(__ballot(ok[s4] && key[s4] >= c));
+    if (cnt >= m) T = c;
+  }
+  int above = 0;
+#pragma unroll
+  for (int s4 = 0; s4 < 4; ++s4) above += __popcll(__ballot(ok[s4] && key[s4] > T));
+  const int rem = m - above;
+  const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  int eq_base = 0, out_base = 0;
+#pragma unroll
+  for (int s4 = 0; s4 < 4; ++s4) {
+    const int j = lane + 64 * s4;
+    const bool eq = ok[s4] && key[s4] == T;
+    const uint64_t eqb = __ballot(eq);
+    const int rank = eq_base + __popcll(eqb & lt);
+    const bool sel = ok[s4] && (key[s4] > T || (eq && rank < rem));
+    const uint64_t sb = __ballot(sel);
+    if (sel) {
+      const int pos = out_base + __popcll(sb & lt);
+      sel_idx[w][pos] = j;
+      sel_key[w][pos] = key[s4];
+    }
+    eq_base += __popcll(eqb);
+    out_base += __popcll(sb);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // Order the m selected entries by target descending, index ascending.
+  int32_t* o = topk + (int64_t)row * k;
+  if (lane < m) {
+    const uint32_t kk = sel_key[w][lane];
+    const int idx = sel_idx[w][lane];
+    int r = 0;
+    for (int t = 0; t < m; ++t) r += (sel_key[w][t] > kk) || (sel_key[w][t] == kk && sel_idx[w][t] < idx);
+    o[r] = idx;
+  }
+  if (lane >= m && lane < k) o[lane] = -1;
+}
+
 template <int D, typename TIn, bool F16, int PASS>
 int launch_mass_w(const MassParams& p, int waves, hipStream_t s) {
   const int64_t grid = ((int64_t)p.B * p.Hkv * p.Qb + 7) / 8 * 8 * p.parts;
@@ -641,7 +773,14 @@ extern "C" int spruce_teacher_targets(const float* mass, int64_t B, int64_t Hq, 
   SPRUCE_REQUIRE(k >= 1 && k <= 64, "k must be in [1, 64], got %lld", (long long)k);
   SPRUCE_REQUIRE(Kb <= kTgtMaxKb, "at most %d key blocks per row are supported", kTgtMaxKb);
   SPRUCE_REQUIRE(B * Hkv * Qb < ((int64_t)1 << 31), "too many rows");
-  hipLaunchKernelGGL(teacher_targets_kernel<true>, dim3((unsigned)(B * Hkv * Qb)), dim3(256), 0, (hipStream_t)stream,
+  const int64_t rows = B * Hkv * Qb;
+  if (Kb <= kTgtWaveKb) {
+    hipLaunchKernelGGL(teacher_targets_wave_kernel<true>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                       (hipStream_t)stream, mass, (int)Hq, (int)Hkv, (int)Qb, (int)Kb, (int)k, eps, (int)rows, target,
+                       row_mass, topk);
+    return check_launch("teacher_targets_wave_kernel");
+  }
+  hipLaunchKernelGGL(teacher_targets_kernel<true>, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream,
                      mass, (int)Hq, (int)Hkv, (int)Qb, (int)Kb, (int)k, eps, target, row_mass, topk);
   return check_launch("teacher_targets_kernel");
 }
@@ -652,7 +791,14 @@ extern "C" int spruce_teacher_group_mass(const float* mass, int64_t B, int64_t H
   SPRUCE_REQUIRE(B >= 1 && Hkv >= 1 && Hq >= Hkv && Hq % Hkv == 0 && Qb >= 1 && Kb >= 1, "invalid shape");
   SPRUCE_REQUIRE(Kb <= kTgtMaxKb, "at most %d key blocks per row are supported", kTgtMaxKb);
   SPRUCE_REQUIRE(B * Hkv * Qb < ((int64_t)1 << 31), "too many rows");
-  hipLaunchKernelGGL(teacher_targets_kernel<false>, dim3((unsigned)(B * Hkv * Qb)), dim3(256), 0,
+  const int64_t rows = B * Hkv * Qb;
+  if (Kb <= kTgtWaveKb) {
+    hipLaunchKernelGGL(teacher_targets_wave_kernel<false>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                       (hipStream_t)stream, mass, (int)Hq, (int)Hkv, (int)Qb, (int)Kb, 0, 0.f, (int)rows, group_mass,
+                       row_mass, nullptr);
+    return check_launch("teacher_targets_wave_kernel");
+  }
+  hipLaunchKernelGGL(teacher_targets_kernel<false>, dim3((unsigned)rows), dim3(256), 0,
                      (hipStream_t)stream, mass, (int)Hq, (int)Hkv, (int)Qb, (int)Kb, 0, 0.f, group_mass, row_mass,
                      nullptr);
   return check_launch("teacher_targets_kernel");
