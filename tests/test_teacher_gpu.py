@@ -16,7 +16,7 @@ import torch
 import oracle.teacher as ot
 from spruce_hip import workloads
 from teacher.chunked_extract import block_mass, chunked_pool
-from teacher.targets import teacher_targets
+from teacher.targets import teacher_group_mass, teacher_targets
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -99,6 +99,38 @@ def test_targets_and_topk():
                 srt = np.sort(et[0, g, i, :n])[::-1]
                 if srt[k - 1] - srt[k] > 1e-4:       # unambiguous boundary: same set as the oracle
                     assert set(got[0, g, i].tolist()) == set(etop[0, g, i].tolist()), (g, i)
+
+
+def test_targets_wave_and_workgroup_kernels_agree():
+    # Rows of up to 256 key blocks take the one-wave targets kernel, longer
+    # rows the workgroup kernel.  A 300-block causal mass whose first 256 rows
+    # and columns are a 256-block mass gives the same targets, row mass,
+    # top-k and group mass on those rows, bit for bit (the extra entries are
+    # zeros); the long rows are also checked against the oracle.
+    gen = torch.Generator().manual_seed(21)
+    H, Hkv, Q, k = 8, 2, 300, 8
+    m = torch.rand(1, H, Q, Q, generator=gen) * 64
+    m[..., 40:48] = m[..., 40:41]                        # ties inside rows
+    m[:, :, 100] = 0.0                                   # an all-zero row
+    m = torch.tril(m)
+    big = teacher_targets(m.to(DEV), Hkv, k=k)
+    small = teacher_targets(m[:, :, :256, :256].contiguous().to(DEV), Hkv, k=k)
+    assert torch.equal(big["target"][:, :, :256, :256], small["target"])
+    assert torch.equal(big["row_mass"][:, :, :256], small["row_mass"])
+    assert torch.equal(big["topk"][:, :, :256], small["topk"])
+    gbig, rbig = teacher_group_mass(m.to(DEV), Hkv)
+    gsmall, rsmall = teacher_group_mass(m[:, :, :256, :256].contiguous().to(DEV), Hkv)
+    assert torch.equal(gbig[:, :, :256, :256], gsmall) and torch.equal(rbig[:, :, :256], rsmall)
+    et, er, _ = ot.targets(m.double().numpy(), Hkv, k=k)
+    _check(big["target"], et, "target, 300 blocks")
+    _check(big["row_mass"], er, "row_mass, 300 blocks")
+    got = big["topk"].cpu().numpy()
+    own = big["target"].cpu().numpy()
+    for g in range(Hkv):
+        for i in range(Q):
+            order = np.argsort(-own[0, g, i, :i + 1], kind="stable")[:k]
+            assert got[0, g, i, :order.size].tolist() == order.tolist(), (g, i)
+            assert np.all(got[0, g, i, order.size:] == -1)
 
 
 def test_full_size_cfg4_every_row():
