@@ -907,17 +907,38 @@ __global__ __launch_bounds__(256) void causal_topk_kernel(const float* __restric
     for (int j = tid; j < n; j += 256)
       if ((keys[j] & mask) == prefix) atomicAdd(&hist[(keys[j] >> sh) & 255], 1);
     __syncthreads();
-    if (tid == 0) {
-      int cum = 0, bin = 0;
-      for (int bb = 255; bb >= 0; --bb) {
-        if (cum + hist[bb] >= rem) {
-          bin = bb;
-          break;
-        }
-        cum += hist[bb];
+    if (tid < 64) {
+      // The bin holding the rem-th largest key, counting from bin 255 down:
+      // lane l takes bins 255 - 4l .. 252 - 4l, the lanes' counts are
+      // prefix-summed from the top, and the lane whose range holds rank rem
+      // finds the bin (the same bin and remainder as a scan from the top).
+      const int b0 = 255 - 4 * tid;
+      const int c0 = hist[b0], c1 = hist[b0 - 1], c2 = hist[b0 - 2], c3 = hist[b0 - 3];
+      const int own = c0 + c1 + c2 + c3;
+      int incl = own;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(incl, off);
+        if (tid >= off) incl += t;
       }
-      sel_bin = bin;
-      sel_rem = rem - cum;
+      int cum = incl - own;  // keys in the bins above this lane's
+      if (cum < rem && rem <= incl) {
+        int bin = b0;
+        if (cum + c0 < rem) {
+          cum += c0;
+          bin = b0 - 1;
+          if (cum + c1 < rem) {
+            cum += c1;
+            bin = b0 - 2;
+            if (cum + c2 < rem) {
+              cum += c2;
+              bin = b0 - 3;
+            }
+          }
+        }
+        sel_bin = bin;
+        sel_rem = rem - cum;
+      }
     }
     __syncthreads();
     prefix |= (uint32_t)sel_bin << sh;

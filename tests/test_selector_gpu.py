@@ -172,6 +172,18 @@ def test_topk_search_boundaries():
     assert np.array_equal(_np(got), osel.topk(s.numpy(), 32))
 
 
+def test_topk_rows_longer_than_1024_blocks():
+    # Rows of more than 1024 key blocks take the LDS radix-select kernel.
+    gen = torch.Generator().manual_seed(13)
+    s = torch.randn(2, 1500, 1500, generator=gen)
+    s[0, 1400, :1401] = torch.round(s[0, 1400, :1401] * 2) / 2    # heavy ties
+    s[0, 1300, torch.randperm(1301, generator=gen)[:40]] = 7.0    # a tie across the top-32 boundary
+    s[1, 1499, :1500] = 0.0
+    s[1, 1499, ::3] = -0.0                                         # +0 / -0 tie, treated as equal
+    got = causal_topk_blocks(s.to(DEV), 32)
+    assert np.array_equal(_np(got), osel.topk(s.numpy(), 32))
+
+
 @pytest.mark.parametrize("k", [1, 8, 32, 64, 65])
 def test_topk_candidate_search_and_its_fallback(k):
     # The top-k search first bounds the k-th key by the k-th largest lane
