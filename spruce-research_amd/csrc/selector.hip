@@ -971,8 +971,8 @@ __global__ __launch_bounds__(256) void causal_topk_kernel(const float* __restric
 // order keys finds the k-th largest key T (the largest T with at least k keys
 // >= T), counting with ballots, or any T with exactly k keys >= T; then an
 // in-order compaction takes every key above T and the lowest-index keys equal
-// to it.  Same result as causal_topk_kernel, without LDS atomics or a serial
-// bin scan.
+// to it.  Same result as causal_topk_kernel, without LDS atomics or
+// workgroup barriers.
 constexpr int kWaveTopkKb = 1024;
 constexpr int kWaveTopkPer = kWaveTopkKb / 64;
 __global__ __launch_bounds__(256) void causal_topk_wave_kernel(const float* __restrict__ scores, int64_t rows,

@@ -172,7 +172,8 @@ def test_topk_search_boundaries():
     assert np.array_equal(_np(got), osel.topk(s.numpy(), 32))
 
 
-def test_topk_rows_longer_than_1024_blocks():
+@pytest.mark.parametrize("k", [32, 100])
+def test_topk_rows_longer_than_1024_blocks(k):
     # Rows of more than 1024 key blocks take the LDS radix-select kernel.
     gen = torch.Generator().manual_seed(13)
     s = torch.randn(2, 1500, 1500, generator=gen)
@@ -180,8 +181,8 @@ def test_topk_rows_longer_than_1024_blocks():
     s[0, 1300, torch.randperm(1301, generator=gen)[:40]] = 7.0    # a tie across the top-32 boundary
     s[1, 1499, :1500] = 0.0
     s[1, 1499, ::3] = -0.0                                         # +0 / -0 tie, treated as equal
-    got = causal_topk_blocks(s.to(DEV), 32)
-    assert np.array_equal(_np(got), osel.topk(s.numpy(), 32))
+    got = causal_topk_blocks(s.to(DEV), k)
+    assert np.array_equal(_np(got), osel.topk(s.numpy(), k))
 
 
 @pytest.mark.parametrize("k", [1, 8, 32, 64, 65])
