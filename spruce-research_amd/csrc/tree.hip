@@ -284,8 +284,36 @@ struct TraverseParams {
   int32_t* out;              // [S, qb, C]
 };
 
+// Scores pairs pr + 64 n (n < NP) of one level into pm.  An invalid or
+// missing pair reads the level's first node (always in range) and its result
+// is dropped.
+template <int PQ, int NP>
+__device__ __forceinline__ void score_pairs(const ScoreParams2& sc, const float* qrow, const float* kl,
+                                            const int* cand, const int* valid, int npairs, int lane,
+                                            float* pm) {
+  for (int pr = lane; pr < npairs; pr += 64 * NP) {
+    int idx[NP], cc[NP];
+    bool ok[NP];
+    const float* kv[NP];
+#pragma unroll
+    for (int n = 0; n < NP; ++n) {
+      const int pn = pr + 64 * n;
+      idx[n] = pn < npairs ? pn / sc.Pk : 0;
+      cc[n] = pn < npairs ? pn - idx[n] * sc.Pk : 0;
+      ok[n] = pn < npairs && valid[idx[n]] != 0;
+      kv[n] = kl + (ok[n] ? ((int64_t)cand[idx[n]] * sc.Pk + cc[n]) * sc.pd : 0);
+    }
+    float m[NP];
+    maxsim_multi<PQ, NP, kTravCW>(qrow, kv, sc.pd, m);
+#pragma unroll
+    for (int n = 0; n < NP; ++n)
+      if (pr + 64 * n < npairs) pm[idx[n] * sc.Pk + cc[n]] = ok[n] ? m[n] : 0.f;
+  }
+}
+
 // One wavefront per (slab, query block) row.  PQ > 0: that many query
-// prototypes, two pairs per lane per step; PQ == 0: any count, one pair.
+// prototypes, two pairs per lane per step (one on levels of at most 64
+// pairs); PQ == 0: any count, one pair.
 template <int PQ>
 __global__ __launch_bounds__(64) void tree_traverse_kernel(const TraverseParams p) {
   extern __shared__ float sh[];
@@ -319,26 +347,12 @@ __global__ __launch_bounds__(64) void tree_traverse_kernel(const TraverseParams 
     const float* kl = sc.kp + (s * sc.N + p.offset[v]) * (int64_t)sc.Pk * sc.pd;
     const int npairs = ncand * sc.Pk;
     if (PQ > 0 && sc.pd % (4 * kTravCW) == 0) {
-      // Pairs pr + 64 n (n < kTravNP); an invalid or missing pair reads the
-      // level's first node (always in range) and its result is dropped.
-      for (int pr = lane; pr < npairs; pr += 64 * kTravNP) {
-        int idx[kTravNP], cc[kTravNP];
-        bool ok[kTravNP];
-        const float* kv[kTravNP];
-#pragma unroll
-        for (int n = 0; n < kTravNP; ++n) {
-          const int pn = pr + 64 * n;
-          idx[n] = pn < npairs ? pn / sc.Pk : 0;
-          cc[n] = pn < npairs ? pn - idx[n] * sc.Pk : 0;
-          ok[n] = pn < npairs && valid[idx[n]] != 0;
-          kv[n] = kl + (ok[n] ? ((int64_t)cand[idx[n]] * sc.Pk + cc[n]) * sc.pd : 0);
-        }
-        float m[kTravNP];
-        maxsim_multi<PQ == 0 ? 1 : PQ, kTravNP, kTravCW>(qrow, kv, sc.pd, m);
-#pragma unroll
-        for (int n = 0; n < kTravNP; ++n)
-          if (pr + 64 * n < npairs) pm[idx[n] * sc.Pk + cc[n]] = ok[n] ? m[n] : 0.f;
-      }
+      // A level with at most 64 pairs (the tree's top levels) takes one pair
+      // per lane: with two, half of every lane's chains would be dropped.
+      if (npairs <= 64)
+        score_pairs<PQ == 0 ? 1 : PQ, 1>(sc, qrow, kl, cand, valid, npairs, lane, pm);
+      else
+        score_pairs<PQ == 0 ? 1 : PQ, kTravNP>(sc, qrow, kl, cand, valid, npairs, lane, pm);
     } else {
       for (int pr = lane; pr < npairs; pr += 64) {
         const int i = pr / sc.Pk, c = pr - (pr / sc.Pk) * sc.Pk;
