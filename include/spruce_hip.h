@@ -295,6 +295,23 @@ int spruce_tree_merge_level(const void* child, int64_t S, int64_t n, int64_t P, 
                             int dtype, void* parent, void* stream);
 
 /*
+ * `levels` consecutive parent levels of the key-axis prototype tree from one
+ * call, each level formed as spruce_tree_merge_level forms it (identical
+ * results).  Replaces build_key_tree's level loop (selector/tree.py:116-145).
+ *   child      [S, n, P, D] contiguous device tensor.
+ *   parents    host array of `levels` device pointers; parents[v] is level
+ *              v + 1 above the child, [S, n_{v+1}, P, D] contiguous, with
+ *              n_{v+1} = ceil(n_v / radix) and n_0 = n.
+ * Wide levels get one launch each (one wavefront per parent); once a level
+ * has no more parents than fit as wavefronts of one workgroup in 64 KB of
+ * LDS (at most 16), it and every level above it share one launch, one
+ * workgroup per slab.  1 <= levels <= 32; other limits as
+ * spruce_tree_merge_level.
+ */
+int spruce_tree_merge_levels(const void* child, int64_t S, int64_t n, int64_t P, int64_t D, int64_t radix,
+                             int dtype, void* const* parents, int64_t levels, void* stream);
+
+/*
  * Top-down beam traversal of the key tree.  Replaces traverse_to_leaf_ids
  * (scripts/eval_tree_traversal.py:59-113).
  *   qp  [S, qb, Pq, p] float32: projected query prototypes (FlatGate.project_queries).

@@ -2,6 +2,7 @@
 // traversal, the deployed route producer.
 //
 //   tree_merge_kernel     one parent level of build_key_tree
+//   tree_merge_top_kernel the narrow levels near the root, in one launch
 //                         (selector/tree.py:79-145, _merge_level_prototypes)
 //   tree_traverse_kernel  traverse_to_leaf_ids
 //                         (scripts/eval_tree_traversal.py:59-113)
@@ -73,14 +74,16 @@ struct MergeParams {
   int vec;            // D % 8 == 0 and child 16-byte aligned: 8-element loads
 };
 
-// One wavefront per (slab, parent node).
-__global__ __launch_bounds__(64) void tree_merge_kernel(const MergeParams p) {
-  extern __shared__ float sh[];
-  const int64_t g = blockIdx.x;
-  const int64_t s = g / p.m;
-  const int j = (int)(g - s * p.m);
-  if (s >= p.S) return;
-  const int lane = threadIdx.x;
+// Orders a wavefront's LDS stores before its later LDS loads.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Parent j of slab s, merged by one wavefront (lane 0..63) in its own LDS
+// region sh of merge_lds_floats(p) floats.
+__device__ __forceinline__ void merge_parent(const MergeParams& p, int64_t s, int j, int lane, float* sh) {
   const int c0 = j * p.radix;
   const int cn = p.n - c0 < p.radix ? p.n - c0 : p.radix;  // valid children
   const int ncand = cn * p.P;
@@ -114,13 +117,13 @@ __global__ __launch_bounds__(64) void tree_merge_kernel(const MergeParams p) {
   } else {
     for (int i = lane; i < ncand * D; i += 64) feat[(i / D) * FS + i % D] = load_elem(p.child, cbase + i, p.dtype);
   }
-  __syncthreads();
+  wave_sync();
   for (int d = lane; d < D; d += 64) {
     float acc = 0.f;
     for (int c = 0; c < cn; ++c) acc = acc + feat[(c * p.P) * FS + d];
     mean[d] = model_round(model_round(acc, p.dtype) / (float)cn, p.dtype);
   }
-  __syncthreads();
+  wave_sync();
   // Distances in registers: lane i holds candidate i's (dims in order).
   float dist = 0.f;
   if (lane < ncand) {
@@ -166,6 +169,51 @@ __global__ __launch_bounds__(64) void tree_merge_kernel(const MergeParams p) {
       for (int d = lane; d < D; d += 64)
         store_elem(p.parent, pbase + (int64_t)(1 + r) * D + d, feat[src * FS + d], p.dtype);
     }
+  }
+}
+
+// One wavefront per (slab, parent node).
+__global__ __launch_bounds__(64) void tree_merge_kernel(const MergeParams p) {
+  extern __shared__ float sh[];
+  const int64_t g = blockIdx.x;
+  const int64_t s = g / p.m;
+  const int j = (int)(g - s * p.m);
+  if (s >= p.S) return;
+  merge_parent(p, s, j, threadIdx.x, sh);
+}
+
+// The narrow levels near the root in one launch, where a launch per level
+// costs more than its work: one workgroup of up to kTopWaves wavefronts per
+// slab; wavefront w merges parents w, w + (wavefronts), ... of a level with
+// merge_parent, and a workgroup barrier separates the levels (a level's
+// parents are the next level's children, read back after the barrier from
+// the same workgroup's stores).
+constexpr int kTopWaves = 16, kMergeTopMax = 32;
+struct MergeTopParams {
+  MergeParams p;                   // S, P, D, radix, dtype
+  int levels;                      // parent levels to form
+  int n[kMergeTopMax + 1];         // node count of each level; n[0] = the input's
+  void* lvl[kMergeTopMax + 1];     // lvl[0] = input, lvl[v] = parent level v
+  int vec[kMergeTopMax];           // the vec flag of level v as a child
+  int wave_lds;                    // LDS floats per wavefront
+};
+
+__global__ __launch_bounds__(64 * kTopWaves) void tree_merge_top_kernel(const MergeTopParams t) {
+  extern __shared__ float sh[];
+  const int64_t s = blockIdx.x;
+  const int nw = (int)(blockDim.x >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int lane = threadIdx.x & 63;
+  float* mine = sh + wave * t.wave_lds;
+  for (int v = 0; v < t.levels; ++v) {
+    MergeParams p = t.p;
+    p.child = t.lvl[v];
+    p.parent = t.lvl[v + 1];
+    p.n = t.n[v];
+    p.m = t.n[v + 1];
+    p.vec = t.vec[v];
+    for (int j = wave; j < p.m; j += nw) merge_parent(p, s, j, lane, mine);
+    __syncthreads();
   }
 }
 
@@ -477,6 +525,55 @@ extern "C" int spruce_tree_merge_level(const void* child, int64_t S, int64_t n, 
   SPRUCE_REQUIRE(lds <= 65536, "radix * P * D too large for one workgroup's LDS (%zu bytes)", lds);
   hipLaunchKernelGGL(tree_merge_kernel, dim3((unsigned)(S * p.m)), dim3(64), lds, (hipStream_t)stream, p);
   return check_launch("tree_merge_kernel");
+}
+
+extern "C" int spruce_tree_merge_levels(const void* child, int64_t S, int64_t n, int64_t P, int64_t D,
+                                        int64_t radix, int dtype, void* const* parents, int64_t levels,
+                                        void* stream) {
+  SPRUCE_REQUIRE(child && parents, "child and parents must be non-null");
+  SPRUCE_REQUIRE(levels >= 1 && levels <= kMergeTopMax, "levels must be in [1, %d], got %lld", kMergeTopMax,
+                 (long long)levels);
+  SPRUCE_REQUIRE(S >= 1 && S < ((int64_t)1 << 31) && n >= 1 && n < ((int64_t)1 << 31),
+                 "S and n must be in [1, 2^31)");
+  for (int v = 0; v < levels; ++v) SPRUCE_REQUIRE(parents[v], "parent level %d is a null pointer", v);
+  const int64_t wave_lds = radix * P * (D + 4) + D;
+  int64_t waves = wave_lds > 0 ? 65536 / (wave_lds * (int64_t)sizeof(float)) : 0;
+  waves = waves > kTopWaves ? kTopWaves : waves;
+  int64_t cur_n = n;
+  const void* cur = child;
+  for (int v = 0; v < levels; ++v) {
+    const int64_t m = (cur_n + radix - 1) / radix;
+    if (m <= waves && radix >= 2 && radix * P <= 64 && P >= 1 && D >= 1 && D <= 256) {
+      // Every remaining level has at most one parent per wavefront.
+      MergeTopParams t{};
+      t.p.S = S;
+      t.p.P = (int)P;
+      t.p.D = (int)D;
+      t.p.radix = (int)radix;
+      t.p.dtype = dtype;
+      t.levels = (int)(levels - v);
+      t.n[0] = (int)cur_n;
+      t.lvl[0] = const_cast<void*>(cur);
+      for (int u = 0; u < t.levels; ++u) {
+        t.n[u + 1] = (t.n[u] + (int)radix - 1) / (int)radix;
+        t.lvl[u + 1] = parents[v + u];
+        t.vec[u] = (D % 8 == 0 && ((uintptr_t)t.lvl[u] % 16) == 0) ? 1 : 0;
+      }
+      SPRUCE_REQUIRE(dtype == SPRUCE_DTYPE_BF16 || dtype == SPRUCE_DTYPE_F16 || dtype == SPRUCE_DTYPE_F32,
+                     "unsupported dtype code %d", dtype);
+      t.wave_lds = (int)wave_lds;
+      const size_t lds = (size_t)waves * wave_lds * sizeof(float);
+      hipLaunchKernelGGL(tree_merge_top_kernel, dim3((unsigned)S), dim3((unsigned)(64 * waves)), lds,
+                         (hipStream_t)stream, t);
+      return check_launch("tree_merge_top_kernel");
+    }
+    // Wide level: one wavefront per parent (checks every argument).
+    const int rc = spruce_tree_merge_level(cur, S, cur_n, P, D, radix, dtype, parents[v], stream);
+    if (rc != 0) return rc;
+    cur = parents[v];
+    cur_n = m;
+  }
+  return 0;
 }
 
 extern "C" int spruce_tree_traverse(const float* qp, const float* kp, int64_t S, int64_t qb, int64_t kb, int64_t Pq,

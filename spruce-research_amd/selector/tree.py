@@ -2,7 +2,9 @@
 
 ``build_key_tree(k_feat [L,G,kb,P,d], radix=2)`` returns the levels
 leaf-first as ``KeyTreeLevel`` (level, features, starts, ends), like the
-reference.  Each parent level is one HIP launch (``spruce_tree_merge_level``):
+reference.  All levels come from one library call
+(``spruce_tree_merge_levels``: a launch per wide level, the narrow levels near
+the root in one launch):
 per parent, prototype 0 is the mean of its children's prototype 0 (summed and
 divided in the model dtype, as the reference does) and prototypes 1..P-1 are
 the child prototypes farthest from it, farthest first.  Node ranges: node i of
@@ -13,6 +15,7 @@ Differences, documented: distances are float32 (the reference computes them
 in the model dtype) and equal distances go to the lower child prototype (the
 reference leaves tie order to ``torch.topk``).
 """
+import ctypes
 from dataclasses import dataclass
 
 import torch
@@ -63,9 +66,25 @@ def level_ranges(num_leaves, level, radix, device=None):
     return starts, (starts + span).clamp_max(num_leaves)
 
 
+_RANGE_TABLES = {}
+
+
 def _level_range_table(num_leaves, radix, device):
     """level_ranges of every level (leaf first), computed on the host and
-    moved to the device in one copy; returns per-level (starts, ends) views."""
+    moved to the device in one copy; returns per-level (starts, ends) views.
+
+    The table depends only on (num_leaves, radix, device), so it is built once
+    per key and shared by every tree built after (its host-to-device copy
+    would otherwise stall the host behind the GPU on every call); the range
+    tensors must not be modified in place."""
+    key = (int(num_leaves), int(radix), str(torch.device(device)))
+    hit = _RANGE_TABLES.get(key)
+    if hit is None:
+        hit = _RANGE_TABLES[key] = _build_level_range_table(num_leaves, radix, device)
+    return hit
+
+
+def _build_level_range_table(num_leaves, radix, device):
     counts, spans = [num_leaves], [1]
     while counts[-1] > 1:
         counts.append((counts[-1] + radix - 1) // radix)
@@ -98,6 +117,33 @@ def merge_level(features, radix=2):
     return out
 
 
+def merge_levels(features, radix=2):
+    """Every parent level above ``features`` up to the root, from one library
+    call (``spruce_tree_merge_levels``: a launch per wide level, then the
+    narrow levels near the root in one launch); each level equals what
+    :func:`merge_level` gives for it."""
+    _validate_radix(radix)
+    if features.dim() != 5:
+        raise ValueError(f"features must be [L,G,n,P,d], got {tuple(features.shape)}")
+    if not features.is_cuda:
+        raise RuntimeError("build_key_tree (HIP) requires GPU tensors")
+    L, G, n, P, d = features.shape
+    x = features.contiguous()
+    outs = []
+    while n > 1:
+        n = (n + radix - 1) // radix
+        outs.append(torch.empty((L, G, n, P, d), device=x.device, dtype=x.dtype))
+    if not outs:
+        return outs
+    ptrs = (ctypes.c_void_p * len(outs))(*[o.data_ptr() for o in outs])
+    with torch.cuda.device(x.device):
+        rc = spruce_hip.lib().spruce_tree_merge_levels(
+            spruce_hip.ptr(x), L * G, x.shape[2], P, d, radix, spruce_hip.dtype_code(x), ptrs, len(outs),
+            spruce_hip.stream_of(x))
+    spruce_hip.check(rc, "spruce_tree_merge_levels")
+    return outs
+
+
 @torch.no_grad()
 def build_key_tree(k_feat, radix=2):
     """Key-node feature levels, leaf-first; odd tails become smaller parents."""
@@ -107,12 +153,8 @@ def build_key_tree(k_feat, radix=2):
     kb = k_feat.shape[2]
     ranges = _level_range_table(kb, radix, k_feat.device)
     levels = [KeyTreeLevel(0, k_feat, *ranges[0])]
-    current = k_feat
-    level = 0
-    while current.shape[2] > 1:
-        level += 1
-        current = merge_level(current, radix)
-        levels.append(KeyTreeLevel(level, current, *ranges[level]))
+    for level, out in enumerate(merge_levels(k_feat, radix), start=1):
+        levels.append(KeyTreeLevel(level, out, *ranges[level]))
     return levels
 
 

@@ -85,6 +85,7 @@ _SIGNATURES = {
         _p, _STRIDES, _p],
     "spruce_residual_frontier": [_p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p],
     "spruce_tree_merge_level": [_p, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _p],
+    "spruce_tree_merge_levels": [_p, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _i64, _p],
     "spruce_tree_traverse": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _p, _i64, _p],
     "spruce_gate_candidate_scores": [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _p, _p],
     "spruce_sparse_prefill_mask": [
