@@ -535,6 +535,10 @@ extern "C" int spruce_tree_merge_levels(const void* child, int64_t S, int64_t n,
                  (long long)levels);
   SPRUCE_REQUIRE(S >= 1 && S < ((int64_t)1 << 31) && n >= 1 && n < ((int64_t)1 << 31),
                  "S and n must be in [1, 2^31)");
+  SPRUCE_REQUIRE(radix >= 2, "radix must be >= 2, got %lld", (long long)radix);
+  SPRUCE_REQUIRE(P >= 1 && D >= 1, "P and D must be positive");
+  SPRUCE_REQUIRE(dtype == SPRUCE_DTYPE_BF16 || dtype == SPRUCE_DTYPE_F16 || dtype == SPRUCE_DTYPE_F32,
+                 "unsupported dtype code %d", dtype);
   for (int v = 0; v < levels; ++v) SPRUCE_REQUIRE(parents[v], "parent level %d is a null pointer", v);
   const int64_t wave_lds = radix * P * (D + 4) + D;
   int64_t waves = wave_lds > 0 ? 65536 / (wave_lds * (int64_t)sizeof(float)) : 0;
@@ -543,7 +547,7 @@ extern "C" int spruce_tree_merge_levels(const void* child, int64_t S, int64_t n,
   const void* cur = child;
   for (int v = 0; v < levels; ++v) {
     const int64_t m = (cur_n + radix - 1) / radix;
-    if (m <= waves && radix >= 2 && radix * P <= 64 && P >= 1 && D >= 1 && D <= 256) {
+    if (m <= waves && radix * P <= 64 && D <= 256) {
       // Every remaining level has at most one parent per wavefront.
       MergeTopParams t{};
       t.p.S = S;
@@ -559,8 +563,6 @@ extern "C" int spruce_tree_merge_levels(const void* child, int64_t S, int64_t n,
         t.lvl[u + 1] = parents[v + u];
         t.vec[u] = (D % 8 == 0 && ((uintptr_t)t.lvl[u] % 16) == 0) ? 1 : 0;
       }
-      SPRUCE_REQUIRE(dtype == SPRUCE_DTYPE_BF16 || dtype == SPRUCE_DTYPE_F16 || dtype == SPRUCE_DTYPE_F32,
-                     "unsupported dtype code %d", dtype);
       t.wave_lds = (int)wave_lds;
       const size_t lds = (size_t)waves * wave_lds * sizeof(float);
       hipLaunchKernelGGL(tree_merge_top_kernel, dim3((unsigned)S), dim3((unsigned)(64 * waves)), lds,
