@@ -80,6 +80,21 @@ def test_packing_and_proto_validation_before_launch():
     assert "not divisible" in spruce_hip.last_error()
 
 
+def test_tree_merge_levels_validation_before_launch():
+    lib = spruce_hip.lib()
+    fake = ctypes.c_void_p(1 << 20)
+    parents = (ctypes.c_void_p * 2)(fake, fake)
+    cases = [((1, 4, 8, 16, 0, 0, parents, 2), "radix must be >= 2"),
+             ((1, 4, 0, 16, 2, 0, parents, 2), "P and D must be positive"),
+             ((1, 4, 8, 16, 2, 9, parents, 2), "unsupported dtype"),
+             ((1, 4, 8, 16, 2, 0, parents, 0), "levels must be in [1, 32]"),
+             ((1, 4, 8, 16, 2, 0, (ctypes.c_void_p * 2)(fake, None), 2), "parent level 1 is a null pointer"),
+             ((1, 4, 40, 16, 2, 0, parents, 2), "radix * P must be <= 64")]
+    for args, message in cases:
+        assert lib.spruce_tree_merge_levels(fake, *args, None) == -1, message
+        assert message in spruce_hip.last_error(), (message, spruce_hip.last_error())
+
+
 def test_error_codes_map_to_reference_exception_types():
     assert _call_index(D=96) == -1
     with pytest.raises(ValueError, match="head_dim"):
