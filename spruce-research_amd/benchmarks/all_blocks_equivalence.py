@@ -11,13 +11,20 @@ hidden relative RMSE <= 0.02, on the last position's logits
 
 The reference loads a checkpoint by hub name and reads prompt manifests;
 neither is available offline, so ``run_equivalence`` takes a loaded model and
-token ids from the caller.
+token ids from the caller.  The reference's manifest and model-loading
+driver (``main``, ``load_manifest``, ``select_matched_records``, ...) is reached
+through the module ``__getattr__`` when its checkout is on ``sys.path``, and
+``python -m benchmarks.all_blocks_equivalence`` runs that driver; its
+attention calls resolve to this package's kernels.
 """
 import math
 
 import torch
 
 from interfaces.validator import PAD_VALUE, validate_selected_blocks
+from spruce_hip.overlay import forward_missing, run_upstream_main
+
+__getattr__ = forward_missing("benchmarks.all_blocks_equivalence", __file__)
 
 DEFAULT_ACCEPTANCE = {
     "require_finite": True,
@@ -142,3 +149,7 @@ def run_equivalence(model, input_ids, *, dense_implementation, sparse_implementa
     layers = [{"layer": i, **tensor_error(s, d)} for (i, s), (_, d) in zip(sparse_layers, dense_layers)]
     return {"logits": logits, "final_hidden": hidden, "layers": layers,
             "accepted": passes_acceptance(logits, hidden, criteria)}
+
+
+if __name__ == "__main__":
+    run_upstream_main("benchmarks.all_blocks_equivalence", __file__, {})

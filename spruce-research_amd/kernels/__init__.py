@@ -2,6 +2,9 @@
 
 Same public names as the reference package (kernels/__init__.py:3-17).
 """
+from pkgutil import extend_path
+
+__path__ = extend_path(__path__, __name__)
 
 from kernels.sparse_prefill import (
     SPRUCE_HIP_SPARSE_PREFILL,

@@ -13,8 +13,8 @@ query row), so no ``[.., C, P, p]`` candidate tensor is ever gathered.
 ``layer_chunk`` is accepted for signature compatibility; nothing is chunked.
 
 Equal scores go to the lower node (the reference leaves tie order to
-``torch.topk``).  ``selector.traversal`` stands in for the reference's
-``scripts/eval_tree_traversal.py`` (this build ships no ``scripts`` package).
+``torch.topk``).  The reference's module name ``scripts.eval_tree_traversal``
+re-exports these functions.
 """
 import math
 

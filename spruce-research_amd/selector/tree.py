@@ -14,6 +14,12 @@ reference's odd-tail rollup.
 Differences, documented: distances are float32 (the reference computes them
 in the model dtype) and equal distances go to the lower child prototype (the
 reference leaves tie order to ``torch.topk``).
+
+The target-side tree and the tree-KL training loss of the reference module
+(``TargetTreeLevel``, ``build_target_tree``, ``iter_tree_levels``,
+``tree_kl_loss``, selector/tree.py:32-43, 148-202, 219-291, 305-) are not part
+of the inference path: those names come from the checkout's selector/tree.py
+through the module ``__getattr__``.
 """
 import ctypes
 from dataclasses import dataclass
@@ -21,6 +27,9 @@ from dataclasses import dataclass
 import torch
 
 import spruce_hip
+from spruce_hip.overlay import forward_missing
+
+__getattr__ = forward_missing("selector.tree", __file__)
 
 
 @dataclass(frozen=True)

@@ -36,11 +36,10 @@ from interfaces.residual_summaries import (build_residual_tree_layout,
                                           validate_residual_summary_nodes)
 from interfaces.validator import validate_selected_blocks
 from kernels.direct_index import direct_index_sparse_prefill, direct_index_sparse_summaries
-from sparse.summaries import build_kv_summary_table
+from sparse.config import SUMMARY_MODES, SUMMARY_PROTOTYPES
+from sparse.summaries import build_kv_summary_table, token_validity_from_attention_mask  # noqa: F401
 
 SPARSE_PREFILL_ATTENTION = "spruce_sparse_prefill"
-SUMMARY_PROTOTYPES = (1, 2, 4)
-SUMMARY_MODES = ("mean", "learned")
 
 
 def _layer_index(module: torch.nn.Module) -> int:

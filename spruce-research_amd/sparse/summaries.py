@@ -18,8 +18,7 @@ import torch
 
 import spruce_hip
 from interfaces.residual_summaries import ResidualTreeLayout
-
-SUMMARY_PROTOTYPES = (1, 2, 4)
+from sparse.config import SUMMARY_PROTOTYPES
 
 
 @dataclass(frozen=True)

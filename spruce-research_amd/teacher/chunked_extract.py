@@ -26,6 +26,9 @@ import torch
 import torch.nn.functional as F
 
 import spruce_hip
+from spruce_hip.overlay import forward_missing
+
+__getattr__ = forward_missing("teacher.chunked_extract", __file__)
 
 _BLOCK = 64
 _PROTO = 8
@@ -319,3 +322,31 @@ def get_pooled_targets(model, tok, prompt, device="cuda", block_size=_BLOCK):
     seq_len = inputs["input_ids"].shape[1]
     pooled, pooled_q, pooled_k = _stack_and_clear_captures(sorted(_CAPTURE))
     return pooled, pooled_q, pooled_k, seq_len
+
+
+@torch.no_grad()
+def get_selector_features(model, tok, prompt, device="cuda", block_size=_BLOCK):
+    """One forward of the base decoder capturing only the selector prototypes
+    (no teacher mass): returns (pooledQ [1, L, G, qb, P, d], pooledK
+    [1, L, G, kb, P, d], both in the model dtype on cpu, seq_len), like the
+    reference's get_selector_features (teacher/chunked_extract.py:268-311)."""
+    if block_size != _BLOCK:
+        raise ValueError("the HIP teacher kernels use block_size=64")
+    _ensure_features_registered()
+    _CAPTURE.clear()
+    _CAPTURE_QK.clear()
+    prev = model.config._attn_implementation
+    _set_attn_impl(model, "selector_feature_capture")
+    try:
+        inputs = tok(prompt, return_tensors="pt").to(device)
+        model.model(**inputs, use_cache=False)
+    finally:
+        _set_attn_impl(model, prev)
+    try:
+        order = sorted(_CAPTURE_QK)
+        pooled_q = torch.stack([_CAPTURE_QK[i][0] for i in order], dim=1)
+        pooled_k = torch.stack([_CAPTURE_QK[i][1] for i in order], dim=1)
+    finally:
+        _CAPTURE.clear()
+        _CAPTURE_QK.clear()
+    return pooled_q, pooled_k, inputs["input_ids"].shape[1]

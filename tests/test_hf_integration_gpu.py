@@ -84,7 +84,7 @@ def test_all_causal_blocks_match_dense_sdpa():
 @torch.no_grad()
 def test_get_pooled_targets_matches_eager_attention_maps():
     from transformers import BatchEncoding
-    from teacher.chunked_extract import get_pooled_targets
+    from teacher.chunked_extract import get_pooled_targets, get_selector_features
     from teacher.extract import get_attentions
     from teacher.pool import pool_attention
     from teacher.validate import check_causal
@@ -98,6 +98,9 @@ def test_get_pooled_targets_matches_eager_attention_maps():
     pooled, pq, pk, seq_len = get_pooled_targets(model, Tok(), prompt, device=DEV)
     assert seq_len == 200 and pooled.shape == (1, 2, 7, 4, 4) and pooled.device.type == "cpu"
     assert pq.shape == (1, 2, 1, 4, 8, 64) and pk.shape == (1, 2, 1, 4, 8, 64) and pq.dtype == torch.float32
+    # The prototypes-only capture (no teacher mass) sees the same layer inputs.
+    fq, fk, n_features = get_selector_features(model, Tok(), prompt, device=DEV)
+    assert n_features == 200 and torch.equal(fq, pq) and torch.equal(fk, pk)
     _set_impl(model, "eager")
     attns, n = get_attentions(model, Tok(), prompt, device=DEV)
     for layer in range(2):
