@@ -12,7 +12,10 @@
  *
  *   pool  : per token, the G query heads of a KV group are summed left to right
  *           (h = 0..G-1); token t of a 64-token block goes to lane t % L (L =
- *           min(64, 256 / (D/8)) lanes per dim), each lane folds its tokens in
+ *           the largest power of two <= min(64, 256 / (D/8)) lanes per dim, so
+ *           that the lanes cover the block and the halving tree every lane;
+ *           tests/test_oracle_selector.py also checks the means against plain
+ *           float64 block means at such D), each lane folds its tokens in
  *           increasing order (starting from the first token's value), lanes are
  *           combined by a halving tree (lane i += lane i + s for s = L/2, L/4,
  *           .., 1), and the block sum is divided (IEEE division) by
@@ -50,7 +53,8 @@ void oracle_block_pool(const float* q, const float* k, int B, int Hq, int Hkv, i
   const int nb = (T + kBlock - 1) / kBlock;
   const int G = Hq / Hkv;
   const int dch = D / 8;
-  const int L = 256 / dch > kBlock ? kBlock : 256 / dch; /* token lanes per dim chunk (<= 64) */
+  int L = kBlock; /* token lanes per dim chunk: a power of two, L * dch <= 256 */
+  while (L > 1 && L * dch > 256) L /= 2;
   const int per = kBlock / L;         /* tokens folded by one lane */
   float lanes[64];
   for (int b = 0; b < B; ++b)

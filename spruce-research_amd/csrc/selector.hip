@@ -6,7 +6,9 @@
 // operations (this file is built with -ffp-contract=off; fused multiply-adds
 // appear only where __builtin_fmaf is written, divisions are IEEE):
 //   pool    per token the G query heads are summed left to right; token t of a
-//           64-token block belongs to lane t % L (L = min(64, 256 / (D/8)));
+//           64-token block belongs to lane t % L (L = the largest power of two
+//           <= min(64, 256 / (D/8)), so L lanes of 64 / L tokens cover the
+//           block exactly and the halving tree reaches every lane);
 //           a lane folds its tokens in increasing order starting from the first
 //           token's value; lanes combine by a halving tree; the sum is divided
 //           by G * (real tokens).  Missing tokens add +0.0f to sums, nothing to
@@ -31,6 +33,14 @@ namespace spruce {
 
 constexpr int kSelBlock = 64;
 
+// Token lanes per 8-dim chunk of the pooling kernels: the largest power of two
+// with lanes * (D / 8) <= 256 threads, at most one lane per token of a block.
+__host__ __device__ constexpr int pool_lanes(int dch) {
+  int lanes = kSelBlock;
+  while (lanes > 1 && lanes * dch > 256) lanes /= 2;
+  return lanes;
+}
+
 struct PoolParams {
   const void* q;
   const void* k;
@@ -54,7 +64,7 @@ __global__ __launch_bounds__(256) void block_pool_kernel(const PoolParams p) {
   __shared__ float red[256 * 8];
   __shared__ float redmax[256 * 8];
   const int dch = p.D / 8;
-  const int L = (256 / dch) > kSelBlock ? kSelBlock : 256 / dch;
+  const int L = pool_lanes(dch);
   const int per = kSelBlock / L;
   const int tid = threadIdx.x;
   const int l = tid / dch, c = tid - (tid / dch) * dch;
@@ -204,7 +214,7 @@ __global__ __launch_bounds__(256) void block_pool_fast_kernel(const PoolParams p
   __shared__ float red[256 * 8];
   __shared__ float redmax[256 * 8];
   const int dch = p.D / 8;
-  const int L = (256 / dch) > kSelBlock ? kSelBlock : 256 / dch;
+  const int L = pool_lanes(dch);
   const int per = kSelBlock / L;
   const int tid = threadIdx.x;
   const int l = tid / dch, c = tid - (tid / dch) * dch;
@@ -1114,7 +1124,7 @@ extern "C" int spruce_selector_pool(const void* q, const int64_t qs[4], const vo
   const int64_t grid = B * Hkv * p.nb;
   SPRUCE_REQUIRE(grid < ((int64_t)1 << 31), "grid too large");
   const int dch = (int)(D / 8);
-  const int L = (256 / dch) > kSelBlock ? kSelBlock : 256 / dch;
+  const int L = pool_lanes(dch);
   if (p.G <= kPoolMaxG && kSelBlock / L <= kPoolMaxPer) {
     if (dtype == SPRUCE_DTYPE_BF16)
       hipLaunchKernelGGL(block_pool_fast_kernel<InBF16>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, p);

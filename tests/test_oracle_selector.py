@@ -37,6 +37,24 @@ def test_full_and_ragged_block_means_and_exact_max():
     assert np.array_equal(k_sum[0, 0, 1, 1], k[0, 0, 64:].max(axis=0))   # pad rows never win
 
 
+@pytest.mark.parametrize("D", [8, 16, 80, 96, 120, 128, 200, 264, 1000, 2048])
+def test_block_mean_and_max_match_plain_block_statistics(D):
+    # The lane layout must cover all 64 tokens of a block at every head_dim the
+    # ABI accepts (multiples of 8 up to 2048), not only powers of two: the
+    # float32 means agree with float64 block means to rounding, the maxima exactly.
+    rng = np.random.default_rng(D)
+    T, G = 64 * 2 + 37, 3
+    q = rng.standard_normal((1, G, T, D)).astype(np.float32)
+    k = rng.standard_normal((1, 1, T, D)).astype(np.float32)
+    q_mean, k_sum = osel.block_pool(q, k)
+    for blk, (a, b) in enumerate(((0, 64), (64, 128), (128, T))):
+        qm = q[0, :, a:b].astype(np.float64).mean(axis=(0, 1))
+        km = k[0, 0, a:b].astype(np.float64).mean(axis=0)
+        np.testing.assert_allclose(q_mean[0, 0, blk], qm, rtol=0, atol=2e-6)
+        np.testing.assert_allclose(k_sum[0, 0, blk, 0], km, rtol=0, atol=2e-6)
+        assert np.array_equal(k_sum[0, 0, blk, 1], k[0, 0, a:b].max(axis=0))
+
+
 def test_integer_valued_pooling_and_projection_are_exact():
     # Small integers: every sum is exact, so only the final division rounds.
     rng = np.random.default_rng(2)

@@ -29,6 +29,9 @@ def _np(t):
     (1, 16, 2, 300, 256, torch.bfloat16),   # G = 8, 8 token steps per thread: the typed kernel's limits
     (1, 18, 2, 150, 128, torch.float16),    # G = 9: the generic kernel
     (1, 4, 2, 100, 512, torch.float32),     # 16 token steps per thread: the generic kernel
+    (1, 12, 2, 150, 96, torch.bfloat16),    # 16 lanes of 12 dim chunks: head_dim not a power of two
+    (1, 8, 4, 129, 80, torch.float16),
+    (1, 4, 1, 70, 2040, torch.float32),     # one lane of 255 dim chunks, 64 token steps
 ])
 def test_pooling_is_bit_exact(B, Hq, Hkv, T, D, dtype):
     gen = torch.Generator().manual_seed(T + D)
@@ -38,6 +41,15 @@ def test_pooling_is_bit_exact(B, Hq, Hkv, T, D, dtype):
     eqm, eks = osel.block_pool(q.float().numpy(), k.float().numpy())
     assert np.array_equal(_np(qm), eqm)
     assert np.array_equal(_np(ks), eks)
+    # Every token of every block is pooled: float64 block means and exact maxima.
+    nb = (T + 63) // 64
+    q64 = q.double().reshape(B, Hkv, Hq // Hkv, T, D).mean(dim=2)
+    for blk in range(nb):
+        sl = slice(64 * blk, min(T, 64 * blk + 64))
+        np.testing.assert_allclose(_np(qm[:, :, blk]), q64[:, :, sl].mean(dim=2).numpy(), rtol=0, atol=5e-6)
+        np.testing.assert_allclose(_np(ks[:, :, blk, 0]), k[:, :, sl].double().mean(dim=2).numpy(),
+                                   rtol=0, atol=5e-6)
+        assert torch.equal(ks[:, :, blk, 1].cpu(), k[:, :, sl].float().amax(dim=2))
     _, ks_only = pool_blocks(None, k.to(DEV))
     assert torch.equal(ks_only, ks)
 
