@@ -505,7 +505,9 @@ extern "C" int spruce_tree_merge_level(const void* child, int64_t S, int64_t n, 
   SPRUCE_REQUIRE(child && parent, "child and parent must be non-null device pointers");
   SPRUCE_REQUIRE(S >= 1 && n >= 1 && P >= 1 && D >= 1, "S, n, P and D must be positive");
   SPRUCE_REQUIRE(radix >= 2, "radix must be >= 2, got %lld", (long long)radix);
-  SPRUCE_REQUIRE(radix * P <= 64, "radix * P must be <= 64, got %lld", (long long)(radix * P));
+  // Each factor is bounded before the product is formed, so it cannot overflow.
+  SPRUCE_REQUIRE(radix <= 64 && P <= 64 && radix * P <= 64, "radix * P must be <= 64, got radix %lld, P %lld",
+                 (long long)radix, (long long)P);
   SPRUCE_REQUIRE(D <= 256, "feature dim must be <= 256, got %lld", (long long)D);
   SPRUCE_REQUIRE(dtype == SPRUCE_DTYPE_BF16 || dtype == SPRUCE_DTYPE_F16 || dtype == SPRUCE_DTYPE_F32,
                  "unsupported dtype code %d", dtype);
@@ -537,6 +539,10 @@ extern "C" int spruce_tree_merge_levels(const void* child, int64_t S, int64_t n,
                  "S and n must be in [1, 2^31)");
   SPRUCE_REQUIRE(radix >= 2, "radix must be >= 2, got %lld", (long long)radix);
   SPRUCE_REQUIRE(P >= 1 && D >= 1, "P and D must be positive");
+  // The per-level limits of spruce_tree_merge_level, checked before any product below is formed.
+  SPRUCE_REQUIRE(radix <= 64 && P <= 64 && radix * P <= 64, "radix * P must be <= 64, got radix %lld, P %lld",
+                 (long long)radix, (long long)P);
+  SPRUCE_REQUIRE(D <= 256, "feature dim must be <= 256, got %lld", (long long)D);
   SPRUCE_REQUIRE(dtype == SPRUCE_DTYPE_BF16 || dtype == SPRUCE_DTYPE_F16 || dtype == SPRUCE_DTYPE_F32,
                  "unsupported dtype code %d", dtype);
   for (int v = 0; v < levels; ++v) SPRUCE_REQUIRE(parents[v], "parent level %d is a null pointer", v);
@@ -547,7 +553,7 @@ extern "C" int spruce_tree_merge_levels(const void* child, int64_t S, int64_t n,
   const void* cur = child;
   for (int v = 0; v < levels; ++v) {
     const int64_t m = (cur_n + radix - 1) / radix;
-    if (m <= waves && radix * P <= 64 && D <= 256) {
+    if (m <= waves) {
       // Every remaining level has at most one parent per wavefront.
       MergeTopParams t{};
       t.p.S = S;
@@ -585,7 +591,8 @@ extern "C" int spruce_tree_traverse(const float* qp, const float* kp, int64_t S,
   SPRUCE_REQUIRE(kb >= 1 && kb < ((int64_t)1 << 30), "key blocks must be in [1, 2^30)");
   SPRUCE_REQUIRE(radix >= 2, "radix must be >= 2, got %lld", (long long)radix);
   SPRUCE_REQUIRE(beam >= 1, "beam must be >= 1, got %lld", (long long)beam);
-  SPRUCE_REQUIRE(beam * radix <= 64, "beam * radix must be <= 64, got %lld", (long long)(beam * radix));
+  SPRUCE_REQUIRE(beam <= 32 && radix <= 64 && beam * radix <= 64,
+                 "beam * radix must be <= 64, got beam %lld, radix %lld", (long long)beam, (long long)radix);
   TraverseParams p{};
   // Level counts ceil(prev / radix) down to one root; node (v, i) has ID offset[v] + i.
   int64_t count = kb, span = 1, total = 0;

@@ -89,10 +89,20 @@ def test_tree_merge_levels_validation_before_launch():
              ((1, 4, 8, 16, 2, 9, parents, 2), "unsupported dtype"),
              ((1, 4, 8, 16, 2, 0, parents, 0), "levels must be in [1, 32]"),
              ((1, 4, 8, 16, 2, 0, (ctypes.c_void_p * 2)(fake, None), 2), "parent level 1 is a null pointer"),
-             ((1, 4, 40, 16, 2, 0, parents, 2), "radix * P must be <= 64")]
+             ((1, 4, 40, 16, 2, 0, parents, 2), "radix * P must be <= 64"),
+             # Factors whose int64 product would overflow are rejected before it is formed.
+             ((1, 4, 1 << 62, 16, 4, 0, parents, 2), "radix * P must be <= 64"),
+             ((1, 4, 1 << 40, 16, 1 << 40, 0, parents, 2), "radix * P must be <= 64"),
+             ((1, 4, 8, 1 << 62, 2, 0, parents, 2), "feature dim must be <= 256")]
     for args, message in cases:
         assert lib.spruce_tree_merge_levels(fake, *args, None) == -1, message
         assert message in spruce_hip.last_error(), (message, spruce_hip.last_error())
+    assert lib.spruce_tree_merge_level(fake, 1, 4, 1 << 62, 16, 4, 0, fake, None) == -1
+    assert "radix * P must be <= 64" in spruce_hip.last_error()
+    # Traversal: beam * radix is bounded the same way.
+    for beam, radix in ((1 << 62, 4), (4, 1 << 62), (33, 2)):
+        assert lib.spruce_tree_traverse(fake, fake, 1, 4, 8, 1, 1, 16, radix, beam, 1.0, fake, 4, None) == -1
+        assert "beam * radix must be <= 64" in spruce_hip.last_error()
 
 
 def test_error_codes_map_to_reference_exception_types():
@@ -113,3 +123,18 @@ def test_kernel_metadata_reports_launch_shape():
     assert {"kwargs", "num_warps", "num_stages", "num_ctas"} <= set(best)
     assert isinstance(best["kwargs"], dict) and best["num_warps"] == best["waves_per_workgroup"]
     assert all(isinstance(best[k], int) for k in ("num_warps", "num_stages", "num_ctas"))
+
+
+def test_noalloc_rejects_shapes_above_the_scratch_limit():
+    # spruce_kv_summary_noalloc checks the scratch size before any HIP call, so
+    # the fake pointers are never used.
+    lib = spruce_hip.lib()
+    limit = 64 << 20
+    assert lib.spruce_kv_summary_workspace_bytes(1, 8, 131072, 128) > limit
+    assert lib.spruce_kv_summary_workspace_bytes(1, 4, 65536, 128) <= limit
+    fake = ctypes.c_void_p(1 << 20)
+    st = (ctypes.c_int64 * 4)(0, 0, 128, 1)
+    rc = lib.spruce_kv_summary_noalloc(fake, st, fake, st, 1, 8, 131072, 128, 0, None, fake, fake, 16,
+                                       fake, fake, fake, fake, None)
+    assert rc == -1
+    assert "above its limit" in spruce_hip.last_error()
