@@ -475,9 +475,14 @@ int spruce_kv_summary(const void* k, const int64_t ks[4], const void* v, const i
  * shapes with spruce_kv_summary_workspace_bytes(B, Hkv, T, D) above it (for
  * example B * Hkv * T > 4 * 65536 at D = 128) return SPRUCE_EINVAL.
  * The current device must be the device of `stream`.  Every call on one GPU
- * shares that buffer: calls that overlap on one GPU (concurrent streams or
- * threads) race and must be serialised by the caller.  Results are identical
- * to spruce_kv_summary's.
+ * shares that buffer, so the calls on one GPU are ordered: each call's
+ * kernels wait (hipStreamWaitEvent on a per-device event, created on the
+ * device's first call) for the previous call's, whatever stream either was
+ * issued on, and calls from several host threads enter one at a time.  A call
+ * issued under stream capture is not ordered this way (the event would tie the
+ * graph to uncaptured work): replays of captured calls that may overlap each
+ * other or uncaptured calls on the same GPU must be serialised by the caller.
+ * Results are identical to spruce_kv_summary's.
  */
 #define SPRUCE_KV_SUMMARY_NOALLOC_MAX_BYTES (64u << 20)
 int spruce_kv_summary_noalloc(const void* k, const int64_t ks[4], const void* v, const int64_t vs[4], int64_t B,

@@ -639,13 +639,21 @@ static __device__ __align__(256) unsigned char scratch[SPRUCE_KV_SUMMARY_NOALLOC
 namespace {
 
 constexpr int kMaxDevices = 64;
+// Guards the per-device tables below, and is held by a call from its ordering
+// wait to its ordering record, so calls from several host threads enter one at
+// a time.
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
+// Recorded after each call's launches; the next call on the device makes its
+// stream wait for it, so calls on different streams do not share the scratch
+// at the same time.
+hipEvent_t g_scratch_done[kMaxDevices] = {};
 
-// Device address of `scratch` on the current device, which must be the
-// device of `stream` (a stream of another device would run the kernels where
-// this address is not mapped).
-int scratch_for_stream(void* stream, void** out) {
+// Device address of `scratch` on the current device and that device's
+// ordering event, set up on the device's first call.  The current device must
+// be the device of `stream` (a stream of another device would run the kernels
+// where this address is not mapped).  The caller holds g_scratch_mu.
+int scratch_for_stream(void* stream, void** out, hipEvent_t* done) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return spruce::set_error((int)e, "hipGetDevice failed: %s", hipGetErrorString(e));
@@ -656,16 +664,21 @@ int scratch_for_stream(void* stream, void** out) {
     if (e != hipSuccess) return spruce::set_error((int)e, "hipStreamGetDevice failed: %s", hipGetErrorString(e));
     SPRUCE_REQUIRE(sdev == dev, "stream belongs to device %d but device %d is current", (int)sdev, dev);
   }
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
     void* ptr = nullptr;
     e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (e != hipSuccess || ptr == nullptr)
       return spruce::set_error(e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol,
                                "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+    hipEvent_t ev = nullptr;
+    e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess)
+      return spruce::set_error((int)e, "hipEventCreateWithFlags failed on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_done[dev] = ev;
     g_scratch_ptr[dev] = ptr;
   }
   *out = g_scratch_ptr[dev];
+  *done = g_scratch_done[dev];
   return 0;
 }
 
@@ -683,9 +696,30 @@ extern "C" int spruce_kv_summary_noalloc(const void* k, const int64_t ks[4], con
                  "spruce_kv_summary_noalloc: this shape needs %zu bytes of scratch, above its limit of %zu bytes "
                  "(use spruce_kv_summary with a caller workspace)",
                  need, (size_t)SPRUCE_KV_SUMMARY_NOALLOC_MAX_BYTES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
   void* ws = nullptr;
-  const int rc = scratch_for_stream(stream, &ws);
+  hipEvent_t done = nullptr;
+  int rc = scratch_for_stream(stream, &ws, &done);
   if (rc) return rc;
-  return kv_summary_run(k, ks, v, vs, B, Hkv, T, D, dtype, valid, range_starts, range_ends, R, keys, values, counts,
-                        log_counts, ws, (size_t)SPRUCE_KV_SUMMARY_NOALLOC_MAX_BYTES, stream);
+  // Under stream capture the event would tie the graph to work outside it:
+  // a captured call is ordered by the caller's graph alone.
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing((hipStream_t)stream, &capture);
+  if (e != hipSuccess) return spruce::set_error((int)e, "hipStreamIsCapturing failed: %s", hipGetErrorString(e));
+  const bool ordered = capture == hipStreamCaptureStatusNone;
+  if (ordered) {
+    // The previous call's kernels on this device (any stream) finish first;
+    // before the first record the wait is already satisfied.
+    e = hipStreamWaitEvent((hipStream_t)stream, done, 0);
+    if (e != hipSuccess) return spruce::set_error((int)e, "hipStreamWaitEvent failed: %s", hipGetErrorString(e));
+  }
+  rc = kv_summary_run(k, ks, v, vs, B, Hkv, T, D, dtype, valid, range_starts, range_ends, R, keys, values, counts,
+                      log_counts, ws, (size_t)SPRUCE_KV_SUMMARY_NOALLOC_MAX_BYTES, stream);
+  if (ordered) {
+    // Recorded whatever rc is: a failed call may have launched some kernels.
+    e = hipEventRecord(done, (hipStream_t)stream);
+    if (e != hipSuccess && rc == 0)
+      return spruce::set_error((int)e, "hipEventRecord failed: %s", hipGetErrorString(e));
+  }
+  return rc;
 }

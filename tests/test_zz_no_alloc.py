@@ -5,10 +5,10 @@ Both entry points run the same kernels, one on a caller workspace and one on
 the library's static scratch, so the bar is bit-exact equality of keys,
 values, counts and log counts.  Two calls in a row on the shared scratch, the
 second with a smaller input (and a padding mask), then a third on the scalar
-path (D = 48); a shape above the scratch limit is rejected before any launch.
+path (D = 48); then two calls issued back to back on two streams with no host
+synchronisation between them, which the library orders on the device.  (The
+rejection of shapes above the scratch limit needs no GPU: tests/test_abi.py.)
 """
-import ctypes
-
 import pytest
 import torch
 
@@ -41,7 +41,7 @@ def _noalloc(key, value, table, valid=None):
     return keys, values, counts, log_counts
 
 
-def _case(T, H, D, dtype, prototypes, masked, seed):
+def _inputs(T, H, D, dtype, prototypes, masked, seed):
     gen = torch.Generator().manual_seed(seed)
     key = torch.randn(1, T, H, D, generator=gen).to(dtype).to(DEV).transpose(1, 2)
     value = torch.randn(1, T, H, D, generator=gen).to(dtype).to(DEV).transpose(1, 2)
@@ -55,11 +55,20 @@ def _case(T, H, D, dtype, prototypes, masked, seed):
     print(f"case T={T} H={H} D={D} {dtype} P={prototypes} masked={masked} scratch={need} bytes", flush=True)
     assert need <= LIMIT
     table = build_kv_summary_table(key, value, layout, block_size=64, prototypes=prototypes, token_mask=valid)
-    got = _noalloc(key, value, table, valid)
-    torch.cuda.synchronize()
+    return key, value, valid, table
+
+
+def _check(got, table):
     for name, a, b in zip(("keys", "values", "counts", "log_counts"), got,
                           (table.keys, table.values, table.counts, table.log_counts)):
         assert torch.equal(a, b), name
+
+
+def _case(T, H, D, dtype, prototypes, masked, seed):
+    key, value, valid, table = _inputs(T, H, D, dtype, prototypes, masked, seed)
+    got = _noalloc(key, value, table, valid)
+    torch.cuda.synchronize()
+    _check(got, table)
 
 
 def test_noalloc_matches_workspace_entry_on_consecutive_calls():
@@ -68,12 +77,17 @@ def test_noalloc_matches_workspace_entry_on_consecutive_calls():
     _case(1000, 3, 48, torch.float32, 1, True, 2)       # scalar chunk path
 
 
-def test_noalloc_rejects_shapes_above_the_scratch_limit():
-    lib = spruce_hip.lib()
-    assert lib.spruce_kv_summary_workspace_bytes(1, 8, 131072, 128) > LIMIT
-    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: the size check fails first
-    st = (ctypes.c_int64 * 4)(0, 0, 128, 1)
-    rc = lib.spruce_kv_summary_noalloc(fake, st, fake, st, 1, 8, 131072, 128, 0, None, fake, fake, 16,
-                                       fake, fake, fake, fake, None)
-    assert rc == -1
-    assert "above its limit" in spruce_hip.last_error()
+def test_noalloc_calls_on_two_streams_are_ordered():
+    big = _inputs(65536, 4, 128, torch.bfloat16, 4, False, 3)
+    small = _inputs(3000, 2, 128, torch.float16, 2, True, 4)
+    torch.cuda.synchronize()
+    streams = (torch.cuda.Stream(), torch.cuda.Stream())   # default priority
+    for order in ((big, small), (small, big)):
+        results = []
+        for stream, (key, value, valid, table) in zip(streams, order):
+            stream.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(stream):
+                results.append(_noalloc(key, value, table, valid))
+        torch.cuda.synchronize()
+        for got, (_, _, _, table) in zip(results, order):
+            _check(got, table)
