@@ -32,11 +32,13 @@
 // summed, so one of two schedules is used:
 //   single pass (when its scratch fits, see kSinglePassScratchMax): online
 //     row reference point and denominator, and for every J the row's partial
-//     sum e_J = sum_j exp2(s_j - m_J) with its reference point m_J written to
-//     scratch (8 bytes per row and J, staged in LDS and copied every kRing
-//     blocks); once the row is complete the wave
-//     reads them back and sums e_J * exp2(m_J - m) / l over its 32 rows in a
-//     fixed butterfly order.  QK^T runs once.
+//     sum e_J = sum_j exp2(s_j - m_r), staged in an LDS ring of kRing blocks
+//     whose entries all share one reference point m_r (a raise of the row's
+//     reference point rescales the ring's earlier entries); a full ring goes
+//     to scratch as 4 bytes per row and J plus m_r once per row and ring, and
+//     the row's last ring stays in LDS.  Once the row is complete the wave
+//     sums e_J * exp2(m_r - m) / l over its 32 rows in a fixed butterfly
+//     order.  QK^T runs once.
 //   two passes (longer sequences): pass 1 keeps only the row reference point
 //     and denominator; pass 2 recomputes the scores and sums exp2(s - m) / l
 //     over each 32-row x 64-key tile.  QK^T runs twice.
@@ -57,25 +59,35 @@ struct MassParams {
   float cs;     // scale * log2(e)
   float* stats;  // [B, Hq, T, 2]: (row max in log2 units, row sum), two-pass only
   float* part;   // [B, Hq, 2, Qb, Qb]
-  float2* rowj;  // single pass: [B, Hq, 2, Qb(Qb+1)/2, 32] (e_J, m_J) per row
+  float* rowe;   // single pass: [B, Hq, 2, Qb(Qb+1)/2, 32] e_J per row (query block I at I(I+1)/2)
+  float* rowm;   // single pass: [B, Hq, 2, ring_slots(Qb), 32] m_r per row and ring
 };
 
-// Single-pass scratch is B*Hq*Qb*(Qb+1)*256 bytes (471 MB at T=16K, 28 heads);
-// above this the two-pass schedule is used instead.
+// Key blocks whose per-row partials a wave stages in LDS before one copy to
+// the single-pass scratch; they share one reference point per row.
+constexpr int kRing = 16;
+
+// Rings of the query blocks before I: sum over i < I of ceil((i + 1) / kRing).
+__host__ __device__ inline int64_t ring_slots(int64_t I) {
+  const int64_t q = I / kRing, r = I % kRing;
+  return kRing * q * (q + 1) / 2 + r * (q + 1);
+}
+
+// Single-pass scratch is B*Hq*(Qb*(Qb+1)*128 + ring_slots(Qb)*256) bytes
+// (243 MB at T=16K, 28 heads); above kSinglePassScratchMax the two-pass
+// schedule is used instead.
 constexpr int64_t kSinglePassScratchMax = (int64_t)4 << 30;
 
+inline int64_t single_pass_e_bytes(int64_t B, int64_t Hq, int64_t Qb) { return B * Hq * Qb * (Qb + 1) * 128; }
+
 inline int64_t single_pass_scratch_bytes(int64_t B, int64_t Hq, int64_t Qb) {
-  return B * Hq * Qb * (Qb + 1) * 256;
+  return single_pass_e_bytes(B, Hq, Qb) + B * Hq * ring_slots(Qb) * 256;
 }
 
 // A half-row block sum above this triggers the max check (the row's
 // reference point is raised only when the block max exceeds it by more than
 // kRescaleThreshold).
 constexpr float kMassCheckSum = 256.0f;
-
-// Key blocks whose per-row partials a wave stages in LDS before one copy to
-// the single-pass scratch.
-constexpr int kRing = 8;
 
 // PASS 1: row statistics; PASS 2: tile mass from them; PASS 3: single pass
 // with per-row partials in the workspace.
@@ -91,9 +103,10 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
   constexpr int EB = TIn::bytes;
 
   __shared__ __attribute__((aligned(16))) uint16_t smem[2 * KTILE];
-  // Single pass: each wave stages its rows' (e_J, m_J) for kRing blocks here
-  // and copies them to the scratch in one go (see flush_ring).
-  __shared__ __attribute__((aligned(16))) float2 ring[PASS == 3 ? WAVES : 1][PASS == 3 ? kRing * 32 : 1];
+  // Single pass: each wave stages its rows' e_J for kRing blocks here, all
+  // relative to the row's current reference point, and copies them to the
+  // scratch in one go (see flush_ring).  Slot J % kRing, row l32.
+  __shared__ __attribute__((aligned(16))) float ring[PASS == 3 ? WAVES : 1][PASS == 3 ? kRing * 32 : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps per-wave addresses scalar
@@ -163,27 +176,32 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
     inv_l = 1.f / stat[1];
   }
   float* part_out = p.part + ((((int64_t)b * p.Hq + head) * 2 + half) * p.Qb + qb) * p.Qb;
-  // Single pass: this tile's (e_J, m_J) rows, J = 0..qb, 32 rows each.
-  float2* rowj = nullptr;
-  if (PASS == 3)
-    rowj = p.rowj + ((((int64_t)b * p.Hq + head) * 2 + half) * ((int64_t)p.Qb * (p.Qb + 1) / 2) +
-                     (int64_t)qb * (qb + 1) / 2) * 32;
+  // Single pass: this tile's e_J rows (J = 0..qb, 32 rows each) and its
+  // per-ring reference points (ring r covers J = r kRing .. r kRing + kRing - 1).
+  float* rowe = nullptr;
+  float* rowm = nullptr;
+  if (PASS == 3) {
+    const int64_t tileh = ((int64_t)b * p.Hq + head) * 2 + half;
+    rowe = p.rowe + (tileh * ((int64_t)p.Qb * (p.Qb + 1) / 2) + (int64_t)qb * (qb + 1) / 2) * 32;
+    rowm = p.rowm + (tileh * ring_slots(p.Qb) + ring_slots(qb)) * 32;
+  }
 
-  // Copies ring slots 0..n-1 (blocks J0..J0+n-1, J0 a multiple of kRing) to
-  // the scratch: 16 bytes per lane per store, kRing * 256 bytes contiguous.
-  // Staging through LDS keeps the global stores to one block in kRing: a
-  // store still in flight makes the next K staging wait for its write
-  // acknowledgement (loads and stores share the counter and may complete
-  // out of order), which per block cost about a tenth of the kernel time.
-  auto flush_ring = [&](int J0, int n) {
+  // Copies the full ring of blocks J0..J0+kRing-1 to the scratch (16 bytes
+  // per lane per store, kRing * 128 bytes contiguous) with the rows'
+  // reference point.  Staging through LDS keeps the global stores to one
+  // block in kRing: a store still in flight makes the next K staging wait for
+  // its write acknowledgement (loads and stores share the counter and may
+  // complete out of order), which per block cost about a tenth of the kernel
+  // time.
+  auto flush_ring = [&](int J0) {
     if constexpr (PASS == 3) {
+      __builtin_amdgcn_wave_barrier();  // the ring's slots were written by the lanes of half 0
       const float4* src = reinterpret_cast<const float4*>(&ring[wave][0]);
-      float4* dst = reinterpret_cast<float4*>(rowj + (int64_t)J0 * 32);
+      float4* dst = reinterpret_cast<float4*>(rowe + (int64_t)J0 * 32);
 #pragma unroll
-      for (int i = 0; i < kRing * 16 / 64; ++i) {
-        const int f = lane + 64 * i;  // float4 index: block f / 16, rows 2(f % 16) and 2(f % 16) + 1
-        if (f < n * 16) dst[f] = src[f];
-      }
+      for (int i = 0; i < kRing * 8 / 64; ++i) dst[lane + 64 * i] = src[lane + 64 * i];
+      if (hl == 0) rowm[(int64_t)(J0 / kRing) * 32 + l32] = m_use;
+      __builtin_amdgcn_wave_barrier();  // the copies are read before the slots are reused
     }
   };
 
@@ -239,7 +257,12 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
         const float delta = (J == 0 || mx > kRescaleThreshold) ? mx : 0.f;
         if (__ballot(delta != 0.f) != 0) {
           m_use += delta;
-          l_run *= fast_exp2(-delta);
+          const float f = fast_exp2(-delta);
+          l_run *= f;
+          if (PASS == 3 && hl == 0 && delta != 0.f) {
+            // The ring's earlier blocks move to the new reference point too.
+            for (int j = 0; j < J % kRing; ++j) ring[PASS == 3 ? wave : 0][j * 32 + l32] *= f;
+          }
           const float nm2 = -m_use;
           ps = fast_exp2(fmaf(s0[0], cs, nm2)) + fast_exp2(fmaf(s1[0], cs, nm2));
 #pragma unroll
@@ -249,8 +272,10 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
       l_run += ps;
       if (PASS == 3) {
         const float e = half_sum(ps);
-        if (hl == 0) ring[PASS == 3 ? wave : 0][(J % kRing) * 32 + l32] = float2{e, m_use};
-        if (J % kRing == kRing - 1) flush_ring(J - (kRing - 1), kRing);
+        if (hl == 0) ring[PASS == 3 ? wave : 0][(J % kRing) * 32 + l32] = e;
+        // A full ring goes to scratch; the row's last ring (the one holding
+        // the diagonal block) stays in LDS for the readback.
+        if (!DIAG && J % kRing == kRing - 1) flush_ring(J - (kRing - 1));
       }
     } else {
       float v = (qtok < p.T) ? ps * inv_l : 0.f;
@@ -280,28 +305,39 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
       stat[1] = lt;
     }
   }
-  if (PASS == 3 && active) {
-    if (qb % kRing != kRing - 1) flush_ring(qb - qb % kRing, qb % kRing + 1);
+  if constexpr (PASS == 3) {
+    if (!active) return;
     const float lt = half_sum(l_run);
     const float inv = (qtok < p.T && lt > 0.f) ? 1.f / lt : 0.f;
     // The wave reads back only what it wrote, on the same CU: a
     // workgroup-scope fence (wait for the stores) orders them before the
     // loads.  An agent-scope fence would also write back this XCD's L2.
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-    // 16 key blocks per step, all loads issued first: lane half hl takes
-    // J = J0 + 2u + hl (u = 0..7), lane l32 row l32; each J is then summed
-    // over the 32 rows by a fixed butterfly.
-    constexpr int U = 8;
+    __builtin_amdgcn_wave_barrier();  // the last ring's slots were written by the lanes of half 0
+    // One ring (16 key blocks) per step, all loads issued first: lane half hl
+    // takes J = J0 + 2u + hl (u = 0..7), lane l32 row l32; each J is then
+    // summed over the 32 rows by a fixed butterfly.  Full rings come from
+    // the scratch, the last one from LDS (relative to the current reference).
+    constexpr int U = kRing / 2;
+    const int Jlast = qb - qb % kRing;
     for (int J0 = 0; J0 <= qb; J0 += 2 * U) {
-      float2 em[U];
+      float e[U];
+      float mr = m_use;
+      if (J0 < Jlast) {
+        mr = rowm[(int64_t)(J0 / kRing) * 32 + l32];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int J = J0 + 2 * u + hl;
-        em[u] = J <= qb ? rowj[(int64_t)J * 32 + l32] : float2{0.f, m_use};
+        for (int u = 0; u < U; ++u) e[u] = rowe[(int64_t)(J0 + 2 * u + hl) * 32 + l32];
+      } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int J = J0 + 2 * u + hl;
+          e[u] = J <= qb ? ring[wave][(J % kRing) * 32 + l32] : 0.f;
+        }
       }
+      const float w = fast_exp2(mr - m_use) * inv;
       float v[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) v[u] = em[u].x * fast_exp2(em[u].y - m_use) * inv;
+      for (int u = 0; u < U; ++u) v[u] = e[u] * w;
 #pragma unroll
       for (int off = 16; off >= 1; off >>= 1)
 #pragma unroll
@@ -713,9 +749,10 @@ extern "C" int spruce_teacher_block_mass_schedule(const void* q, const int64_t q
   p.cs = scale * 1.4426950408889634f;
   hipStream_t s = (hipStream_t)stream;
   if (schedule == SPRUCE_TEACHER_SCRATCH) {
-    // [part: B*Hq*2*Qb*Qb floats][rowj: scratch bytes], rowj 256-byte aligned.
+    // [part: B*Hq*2*Qb*Qb floats][rowe: e_J floats][rowm: m_r floats], each 256-byte aligned.
     p.part = workspace;
-    p.rowj = reinterpret_cast<float2*>(reinterpret_cast<char*>(workspace) + part_bytes(B, Hq, Qb));
+    p.rowe = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + part_bytes(B, Hq, Qb));
+    p.rowm = reinterpret_cast<float*>(reinterpret_cast<char*>(p.rowe) + single_pass_e_bytes(B, Hq, Qb));
     rc = launch_mass<3>(p, (int)D, dtype, shape.waves, s);
     if (rc) return rc;
   } else {
