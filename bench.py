@@ -1,20 +1,21 @@
 """Sparse-prefill benchmark on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--csr128k/--no-csr128k]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-csr128k] [--no-extra]
 
 One step = one block-sparse causal GQA prefill of a Qwen2-7B-shaped attention
-layer (BASELINE cfg2: T=32768, 28 query / 4 KV heads, d=128, bf16 Q/K/V ~
+layer (the headline configuration cfg2: T=32768, 28 query / 4 KV heads, d=128, bf16 Q/K/V ~
 N(0,1) with RoPE theta=1e6, block mask of sink + local-4 + stable top-k at
 ~10% causal density), launched through the C ABI
 (spruce_sparse_prefill_mask) with inputs already resident in HBM.
 
-Printed: one JSON line with the BASELINE metric (effective TFLOP/s over the
+Printed: one JSON line with the headline metric (effective TFLOP/s over the
 computed blocks, 4*64*64*128 FLOP per (query head, selected block)), ms per
 step, the live roofline of the kernel (HIP events on the launch stream) and a
 CPU baseline (the float32 numpy oracle on a bounded sample of the same
-workload).  The 128K direct-index CSR configuration (BASELINE cfg5), the
-selector front end (cfg3, HBM-bound: GB/s) and teacher block-mass extraction
-(cfg4) are timed the same way and reported under "configs".
+workload).  The reference's small fp32 case (cfg1), the 128K direct-index CSR
+configuration (cfg5) with its tree-route producer stage by stage, the selector
+front end (cfg3, HBM-bound: GB/s) and teacher block-mass extraction (cfg4) are
+timed the same way and reported under "configs".
 """
 import argparse
 import json
@@ -29,6 +30,7 @@ for _p in (os.path.join(ROOT, "spruce-research_amd"), ROOT):
         sys.path.insert(0, _p)
 
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_FP32_TFLOPS = 157.3   # MI355X fp32 (vector, with packed FP32)
 PEAK_HBM_GBS = 8000.0
 BLOCK_FLOPS = 4.0 * 64 * 64 * 128  # per (query head, selected 64-key block), d=128
 
@@ -122,6 +124,18 @@ def cpu_baseline(q, k, v, mask_kv, sample_blocks):
         "sample": (f"oracle/attention.py float32 numpy, {len(sample_blocks)} of 512 query blocks "
                    f"x 4 KV heads x 7 query heads of cfg2, {sel * G} head-blocks"),
     }
+
+
+def cpu_baseline_cfg1(q1, k1, v1, mask1, flops):
+    """cfg1 on the host, the whole configuration: the float32 numpy oracle
+    (oracle/attention.py, the reference's PyTorch path restated), median of 3."""
+    import oracle.attention as ora
+    qn, kn, vn, mn = (x.numpy() for x in (q1, k1, v1, mask1))
+    dt = _cpu_time(lambda: ora.sparse_attention_mask(qn, kn, vn, mn))
+    return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "ms": round(dt * 1e3, 2),
+            "cores": _numpy_threads() or os.cpu_count(), "cpu_model": _cpu_model(), "kind": "port",
+            "seconds": round(dt, 3),
+            "sample": "whole cfg1 (8 query heads x 64 query blocks), float32 numpy, median of 3"}
 
 
 def cpu_baseline_selector(q3, k3, Wq, Wk, top_k, nbytes):
@@ -236,6 +250,30 @@ def main():
         }
     }
 
+    # ---- cfg1: the reference's CPU-runnable case (T=4096, 8 query / 2 KV
+    # heads, fp32 N(0,1) Q/K/V, top-16 + sink + diagonal per KV head, bool
+    # mask [1, 8, 64, 64]); fp32 inputs are rounded to bf16 for the matrix cores.
+    q1, k1, v1 = workloads.qkv(args.seed, 4096, 8, 2, D, torch.float32, use_rope=False)
+    mask1 = workloads.cfg1_mask(args.seed)
+    q1d, k1d, v1d, m1d = (x.to(dev) for x in (q1, k1, v1, mask1))
+    sel1 = int(mask1.sum())
+    flops1 = sel1 * BLOCK_FLOPS
+    fn1 = lambda: block_sparse_prefill(q1d, k1d, v1d, m1d, scale)  # noqa: E731
+    _, k1ms = _time_launches(fn1, max(10, args.steps // 2), max(3, args.warmup // 2))
+    m1 = statistics.median(k1ms)
+    configs["cfg1_4k_block_mask_fp32"] = {
+        "ms_median": round(m1, 4), "ms_min": round(min(k1ms), 4), "ms_max": round(max(k1ms), 4),
+        "tflops": round(flops1 / (m1 * 1e-3) / 1e12, 2),
+        "frac_bf16_peak": round(flops1 / (m1 * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "selected_head_blocks": sel1, "flop": flops1, "input_dtype": "fp32",
+        "note": "1 workgroup per (KV head, query block, part): 256 workgroups fill at most a quarter "
+                "of the 256 CUs' slots for a few blocks each, so this small case is launch- and "
+                "latency-bound",
+    }
+    if not args.no_cpu:
+        configs["cfg1_4k_block_mask_fp32"]["cpu_baseline"] = cpu_baseline_cfg1(q1, k1, v1, mask1, flops1)
+    del q1d, k1d, v1d, m1d
+
     # ---- cfg5: T=131072 direct-index CSR with log-normal row densities
     if not args.no_csr128k:
         T5 = 131072
@@ -263,32 +301,80 @@ def main():
         # Tree route producer at the cfg5 grid (deployed settings of the
         # reference's export script: radix 2, beam 16, local window 1,
         # k_selected = beam + 2): prototype features of Q and K, the key tree,
-        # projections, beam traversal and packing into selected_blocks.
+        # projections, beam traversal and packing into selected_blocks.  The
+        # whole route is timed, then each stage on its own (inputs from one
+        # untimed run), each against the roofline of its algorithmic work.
         if not args.no_extra:
             import math
             from interfaces.packing import selected_ids_to_blocks
             from selector.gate import FlatGate
-            from selector.traversal import traverse_to_leaf_ids
+            from selector.traversal import traverse_projected
             from selector.tree import build_key_tree
             from teacher.chunked_extract import _proto_pool_seq, proto_pool_grouped
             kb5, beam = T5 // 64, 16
             gate = FlatGate(1, D, proj_dim=D).to(dev).eval()
+            div = math.sqrt(gate.proj_dim)
+
+            def features():
+                return proto_pool_grouped(q5, Hkv, 64, 8), _proto_pool_seq(k5, 64, 8)
+
+            def project(qf, levels):
+                return (gate.project_queries(qf),
+                        gate.project_keys(torch.cat([lvl.features for lvl in levels], dim=2)))
 
             def route():
-                qf = proto_pool_grouped(q5, Hkv, 64, 8)
-                kf = _proto_pool_seq(k5, 64, 8)
+                qf, kf = features()
                 levels = build_key_tree(kf, radix=2)
-                ids = traverse_to_leaf_ids(gate, qf, levels, beam, radix=2)
+                qp, kp = project(qf, levels)
+                ids = traverse_projected(qp, kp, kb5, beam, 2, div)
                 return selected_ids_to_blocks(ids, beam + 2, local_window=1, key_blocks=kb5)
 
-            _, krms = _time_launches(route, max(5, args.steps // 5), max(2, args.warmup // 5))
+            rsteps, rwarm = max(5, args.steps // 5), max(2, args.warmup // 5)
+            _, krms = _time_launches(route, rsteps, rwarm)
+            qf, kf = features()
+            levels = build_key_tree(kf, radix=2)
+            qp, kp = project(qf, levels)
+            ids = traverse_projected(qp, kp, kb5, beam, 2, div)
+            stage_fns = {
+                "features": features,
+                "tree": lambda: build_key_tree(kf, radix=2),
+                "project": lambda: project(qf, levels),
+                "traverse": lambda: traverse_projected(qp, kp, kb5, beam, 2, div),
+                "pack": lambda: selected_ids_to_blocks(ids, beam + 2, local_window=1, key_blocks=kb5),
+            }
+            work = workloads.tree_route_work(T5, Hq, Hkv, D, P=8, proj=D, beam=beam, radix=2,
+                                             k_selected=beam + 2)
+            stages, floor_ms = {}, 0.0
+            for name, sfn in stage_fns.items():
+                _, sms = _time_launches(sfn, rsteps, rwarm)
+                msd = statistics.median(sms)
+                w = work[name]
+                t_hbm = w["bytes"] / (PEAK_HBM_GBS * 1e9) * 1e3
+                t_fp32 = w["flop"] / (PEAK_FP32_TFLOPS * 1e12) * 1e3
+                bound = "fp32" if t_fp32 > t_hbm else "hbm"
+                floor = max(t_hbm, t_fp32)
+                floor_ms += floor
+                stages[name] = {"ms_median": round(msd, 4), "bytes": w["bytes"], "flop": w["flop"],
+                                "bound": bound, "floor_ms": round(floor, 4),
+                                "frac": round(floor / msd, 4)}
+                if bound == "fp32":
+                    stages[name]["tflops"] = round(w["flop"] / (msd * 1e-3) / 1e12, 2)
+                else:
+                    stages[name]["gbps"] = round(w["bytes"] / (msd * 1e-3) / 1e9, 1)
+            stages["traverse"]["candidates_per_row"] = work["traverse"]["candidates_per_row"]
             mr = statistics.median(krms)
             configs["cfg5_tree_route"] = {
                 "ms_median": round(mr, 4), "ms_min": round(min(krms), 4), "ms_max": round(max(krms), 4),
+                "floor_ms": round(floor_ms, 4), "frac": round(floor_ms / mr, 4),
                 "key_blocks": kb5, "kv_groups": Hkv, "prototypes": 8, "proj_dim": D, "beam": beam,
                 "radix": 2, "k_selected": beam + 2,
-                "stages": "proto features (Q group-avg + K) -> build_key_tree -> project -> traverse -> pack",
+                "stages": stages,
+                "note": ("floor = sum over stages of max(bytes / 8 TB/s, flop / 157.3 TFLOP/s fp32); "
+                         "traverse is the dominant kernel (tree_traverse_kernel, fp32 VALU dot products; "
+                         "157.3 TFLOP/s assumes packed FP32, which this build does not emit, so 78.6 is "
+                         "its VALU ceiling)"),
             }
+            del qf, kf, levels, qp, kp, ids
         del q5, k5, v5
 
     # ---- capture pass: dense causal cfg2 layer that also emits the selector

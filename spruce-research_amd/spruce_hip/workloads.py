@@ -173,3 +173,44 @@ def teacher_flops(T, H, block=BLOCK, D=128):
     """Algorithmic FLOPs of teacher mass: 2*64*64*D per (query head, causal block pair)."""
     qb = (T + block - 1) // block
     return 2.0 * block * block * D * H * qb * (qb + 1) // 2
+
+
+def tree_route_work(T, Hq, Hkv, D, P=8, proj=128, beam=16, radix=2, k_selected=18, elem_bytes=2):
+    """Algorithmic work of each stage of the deployed tree route (prototype
+    features -> key tree -> projections -> beam traversal -> packing), one
+    layer, batch 1.  Returns {stage: {"bytes": compulsory HBM bytes,
+    "flop": arithmetic}}:
+
+    * features: read Q and K once, write the Q and K prototypes
+      ([Hkv, nb, P, D] each, model dtype);
+    * tree: read the leaf prototypes, write every upper level;
+    * project: read the query prototypes and every tree node's prototypes
+      (model dtype), write them projected (float32); 2 * D * proj FLOP per
+      prototype row;
+    * traverse: read the projected tables once, write the leaf ids; per
+      query row and tree level the reference scores width * radix candidates
+      (scripts/eval_tree_traversal.py:84-113), each P x P prototype pairs of
+      2 * proj FLOP;
+    * pack: read the int64 leaf ids, write int32 selected_blocks rows.
+    """
+    nb = (T + BLOCK - 1) // BLOCK
+    counts = [nb]
+    while counts[-1] > 1:
+        counts.append((counts[-1] + radix - 1) // radix)
+    nodes = sum(counts)
+    width, candidates = 1, 0
+    for n in reversed(counts[:-1]):
+        candidates += width * radix
+        width = min(beam, width * radix, n)
+    rows = Hkv * nb
+    feat_row = P * D * elem_bytes
+    return {
+        "features": {"bytes": (Hq + Hkv) * T * D * elem_bytes + 2 * rows * feat_row, "flop": 0},
+        "tree": {"bytes": Hkv * nodes * feat_row, "flop": 0},
+        "project": {"bytes": Hkv * (nb + nodes) * (feat_row + P * proj * 4),
+                    "flop": 2.0 * D * proj * Hkv * (nb + nodes) * P},
+        "traverse": {"bytes": Hkv * (nb + nodes) * P * proj * 4 + rows * width * 8,
+                     "flop": 2.0 * proj * P * P * candidates * rows,
+                     "candidates_per_row": candidates, "width": width},
+        "pack": {"bytes": rows * width * 8 + rows * k_selected * 4, "flop": 0},
+    }

@@ -91,7 +91,7 @@ def test_reference_parity_case_across_blocks(variant):
 
 
 def test_cfg1_block_mask_fp32_inputs():
-    # BASELINE cfg1: T=4096, 8q/2kv, d=128, fp32 N(0,1), top-16 + sink + diagonal.
+    # Benchmark configuration cfg1: T=4096, 8q/2kv, d=128, fp32 N(0,1), top-16 + sink + diagonal.
     q, k, v = workloads.qkv(0, 4096, 8, 2, 128, torch.float32, use_rope=False)
     mask = workloads.cfg1_mask(0)
     expected = ora.sparse_attention_mask(q.numpy(), k.numpy(), v.numpy(), mask.numpy())
@@ -225,7 +225,7 @@ def test_sparse_attention_entry_point_drop_in():
 
 
 def test_full_size_cfg2_every_row_and_layout_identity():
-    # BASELINE cfg2 at full size: T=32768, 28q/4kv, bf16 + RoPE, ~10% density.
+    # Benchmark configuration cfg2 at full size: T=32768, 28q/4kv, bf16 + RoPE, ~10% density.
     print("cfg2: generating inputs", flush=True)
     q, k, v = workloads.qkv(0, 32768, 28, 4, 128, torch.bfloat16, use_rope=True, layout="bthd")
     mask, density = workloads.cfg2_mask(0)
@@ -245,7 +245,7 @@ def test_full_size_cfg2_every_row_and_layout_identity():
 
 
 def test_full_size_cfg5_csr_every_row():
-    # BASELINE cfg5 at full size: T=131072 CSR, log-normal density (median 2%).
+    # Benchmark configuration cfg5 at full size: T=131072 CSR, log-normal density (median 2%).
     # Every query block of every KV head against the oracle, in chunks of 256
     # query blocks (a progress line after each).
     print("cfg5: generating inputs", flush=True)

@@ -26,6 +26,8 @@ matrix cores), which keeps torch's eager bf16 batched products out of the test.
   judged by passes_acceptance against dense attention computed in float32
   (benchmarks/all_blocks_equivalence.py, the reference's criteria).
 """
+import math
+
 import pytest
 import torch
 
@@ -178,9 +180,13 @@ def test_reference_acceptance_gate_at_qwen2_7b_attention_shape(backend, dtype):
     # rounding of every later bf16 op, so both runs' own bf16 noise is in the
     # error.  float32 weights: the dense side sees the same bf16-rounded
     # Q/K/V the kernel feeds its matrix cores, so the error is the kernel's
-    # alone (P rounded to bf16 before P.V, accumulation order); it must also
-    # stay within 5e-3 relative RMSE after the 4 layers (measured 3.5e-3;
-    # 2.2e-3 after the first layer) with the top-10 set unchanged.
+    # alone: P rounded to bf16 before P.V (and the fp32 accumulation order).
+    # Error model for that case: rounding each p_j to bf16 perturbs it by at
+    # most the unit roundoff u = 2^-8, so a layer's attention output moves by
+    # at most u relative; the layers' roundings are independent, so after L
+    # layers the final hidden relative RMSE stays within u * sqrt(L) (7.8e-3
+    # at L = 4; measured 2.2e-3 after the first layer, 3.5e-3 after four),
+    # with the top-10 set unchanged.
     from transformers import AttentionInterface, Qwen2Config, Qwen2ForCausalLM
     from benchmarks.all_blocks_equivalence import run_equivalence
     if backend == "kernels.sparse_prefill":
@@ -209,6 +215,7 @@ def test_reference_acceptance_gate_at_qwen2_7b_attention_shape(backend, dtype):
           flush=True)
     assert result["accepted"], (lg, fh)
     if dtype == torch.float32:
-        assert fh["relative_rmse"] <= 5e-3 and lg["top10_overlap"] == 1.0, (lg, fh)
+        bound = 2.0 ** -8 * math.sqrt(cfg.num_hidden_layers)
+        assert fh["relative_rmse"] <= bound and lg["top10_overlap"] == 1.0, (lg, fh, bound)
     del model
     torch.cuda.empty_cache()

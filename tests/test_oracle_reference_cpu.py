@@ -114,7 +114,7 @@ def _score_error_bound(q, k, Wq, Wk):
 
 
 def test_cfg3_selection_robust_to_the_reference_op_order():
-    # BASELINE cfg3 shape; CPU draws (a different stream from the GPU bench).
+    # Benchmark configuration cfg3 shape; CPU draws (a different stream from the GPU bench).
     q, k, _ = workloads.qkv(0, 65536, 28, 4, 128, torch.bfloat16, use_rope=False)
     Wq, Wk = workloads.cfg3_gate_weights(0)
     top = 32

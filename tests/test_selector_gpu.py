@@ -233,7 +233,7 @@ def test_flat_gate_matches_reference_bruteforce():
 
 
 def test_cfg3_full_size_selected_blocks_bit_exact():
-    # BASELINE cfg3: T=65536 (1024 key blocks), 28 Q / 4 KV heads, d=128, bf16, top-32.
+    # Benchmark configuration cfg3: T=65536 (1024 key blocks), 28 Q / 4 KV heads, d=128, bf16, top-32.
     print("cfg3: generating inputs", flush=True)
     q, k, _ = workloads.qkv(0, 65536, 28, 4, 128, torch.bfloat16, use_rope=False, layout="bthd")
     Wq, Wk = workloads.cfg3_gate_weights(0)

@@ -5,7 +5,7 @@ float64 oracle on the same (bf16/f16-rounded) inputs.  The top-k target
 indices must equal a stable descending argsort of the kernel's own targets
 exactly (ties to the lower block index), and the oracle's wherever its k-th
 and (k+1)-th targets differ by more than the target tolerance.  Full size
-(BASELINE cfg4: T=16384, 28/4 heads, d=128): mass invariants (rows sum to
+(benchmark configuration cfg4: T=16384, 28/4 heads, d=128): mass invariants (rows sum to
 64, zero upper triangle), every (head, query block) row against the oracle,
 and targets / top-k of every row against the oracle's targets of the same mass.
 """
@@ -135,7 +135,7 @@ def test_targets_wave_and_workgroup_kernels_agree(H, Hkv):
 
 
 def test_full_size_cfg4_every_row():
-    # BASELINE cfg4: T=16384 (256 blocks), 28 Q / 4 KV heads, d=128, bf16 with RoPE.
+    # Benchmark configuration cfg4: T=16384 (256 blocks), 28 Q / 4 KV heads, d=128, bf16 with RoPE.
     print("cfg4: generating inputs", flush=True)
     q, k, _ = workloads.qkv(0, 16384, 28, 4, 128, torch.bfloat16, use_rope=True, layout="bthd")
     mass = chunked_pool(q.transpose(1, 2).contiguous().to(DEV).transpose(1, 2), k.to(DEV), 128 ** -0.5)
