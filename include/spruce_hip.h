@@ -256,6 +256,25 @@ int spruce_gate_project2(const float* xa, const float* wa, int64_t Na, const flo
                          int64_t Nb, int64_t D, int64_t P, float* outa, float* outb, void* stream);
 
 /*
+ * The projection of spruce_gate_project applied to prototype rows that sit in
+ * several model-dtype buffers, written as one float32 table: level v's buffer
+ * levels[v] holds [S, level_nodes[v], Pk, D] (contiguous, dtype bf16 / f16 /
+ * f32, 8-byte aligned for 16-bit types, 16-byte for f32), and out
+ * [S, N, Pk, P] (N = sum of level_nodes) takes the levels' nodes in order
+ * (node IDs leaf-first for a key tree).  Every value is widened to float32
+ * exactly, so the results equal spruce_gate_project's on a float32 copy of
+ * the concatenated levels.  Replaces FlatGate.project_keys over the levels of
+ * the key tree (selector/gate.py:124-127, called per level by
+ * scripts/eval_tree_traversal.py:96) and, with one level,
+ * FlatGate.project_queries (:120-122) on model-dtype prototypes.
+ * Errors: 0 or more than 32 levels, D or P not multiples of 4, misaligned
+ * buffers.
+ */
+int spruce_gate_project_levels(const void* const* levels, const int64_t* level_nodes, int64_t nlevels, int64_t S,
+                               int64_t Pk, int64_t D, int dtype, const float* w, int64_t P, float* out,
+                               void* stream);
+
+/*
  * MaxSim block scores: scores[s][i][j] = max over prototype pairs (a, c) of
  * qp[s][i][a] . kp[s][j][c], divided by div (= sqrt(P)).  causal = 1: only
  * j <= i is computed and j > i is written as -inf; causal = 2 with Qb == Kb:

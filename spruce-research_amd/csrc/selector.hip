@@ -514,9 +514,58 @@ constexpr int kBD = 32;
 // tiles). Measured at p = d = 128: N = 131072 0.102 -> 0.068 ms, N = 65536
 // 0.056 -> 0.039 ms; 8 x 8 and 4 x 8 within 5% of 8 x 4.
 constexpr int kBlockProjectRows = 16384, kBlockProjectTR = 8, kBlockProjectTC = 4;
-template <int TR, int TC>
-__global__ __launch_bounds__(256) void project_block_kernel(const float* __restrict__ x, const float* __restrict__ w,
-                                                            int64_t N, int D, int P, float* __restrict__ out) {
+
+// Input rows of project_block_kernel: row n of one contiguous float32 [N, D]
+// buffer ...
+struct ProjRowsF32 {
+  const float* x;
+  __device__ const void* row(int64_t n, int D) const { return x + n * D; }
+};
+
+// ... or of prototype buffers in the model dtype, one per tree level: output
+// row ((s * N + node) * P + proto) reads level v's [S, n_v, P, D] buffer at
+// node - off[v].  Each value is widened to float32 exactly, so the chains see
+// the same operands as after a float32 copy.
+constexpr int kProjMaxSeg = 32;
+struct ProjSegs {
+  const void* base[kProjMaxSeg];
+  int64_t off[kProjMaxSeg + 1];  // level v holds nodes off[v] .. off[v + 1] - 1; off[nseg] = N
+  int nseg, P;
+  int64_t N;
+};
+template <typename TIn>
+struct ProjRowsSeg {
+  ProjSegs g;
+  __device__ const void* row(int64_t n, int D) const {
+    const int64_t np = g.N * g.P;
+    const int64_t sl = n / np, rem = n - sl * np;
+    const int64_t node = rem / g.P, proto = rem - node * g.P;
+    int v = 0;
+    while (v + 1 < g.nseg && node >= g.off[v + 1]) ++v;
+    const int64_t nv = g.off[v + 1] - g.off[v];
+    return static_cast<const char*>(g.base[v]) + ((sl * nv + node - g.off[v]) * g.P + proto) * D * TIn::bytes;
+  }
+};
+
+// Four consecutive input values at element e of a row, widened to float32.
+__device__ __forceinline__ float4 load4_row(const ProjRowsF32&, const void* row, int e) {
+  return *reinterpret_cast<const float4*>(static_cast<const float*>(row) + e);
+}
+template <typename TIn>
+__device__ __forceinline__ float4 load4_row(const ProjRowsSeg<TIn>&, const void* row, int e) {
+  if constexpr (TIn::bytes == 4) {
+    return *reinterpret_cast<const float4*>(static_cast<const float*>(row) + e);
+  } else {
+    constexpr bool F16 = TIn::code == SPRUCE_DTYPE_F16;
+    const uint2 w = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(row) + e);
+    return float4{unpack1<F16>(w.x & 0xffffu), unpack1<F16>(w.x >> 16), unpack1<F16>(w.y & 0xffffu),
+                  unpack1<F16>(w.y >> 16)};
+  }
+}
+
+template <int TR, int TC, typename Rows>
+__global__ __launch_bounds__(256) void project_block_kernel(const Rows src, const float* __restrict__ w, int64_t N,
+                                                            int D, int P, float* __restrict__ out) {
   constexpr int R = 16 * TR, C = 16 * TC;          // workgroup tile
   constexpr int XL = R * kBD / 4 / 256;            // x float4 per thread per slice
   constexpr int WL = C * kBD / 4 / 256;            // w float4 per thread per slice
@@ -531,15 +580,21 @@ __global__ __launch_bounds__(256) void project_block_kernel(const float* __restr
   for (int a = 0; a < TR; ++a)
 #pragma unroll
     for (int c = 0; c < TC; ++c) acc[a][c] = 0.f;
+  // The rows this thread stages are the same in every slice.
+  const void* xrow[XL];
+#pragma unroll
+  for (int t = 0; t < XL; ++t) {
+    const int64_t n = n0 + (tid + 256 * t) / (kBD / 4);
+    xrow[t] = n < N ? src.row(n, D) : nullptr;
+  }
   for (int d0 = 0; d0 < D; d0 += kBD) {
     const int dn = D - d0 < kBD ? D - d0 : kBD;
     float4 xv[XL], wv[WL];
 #pragma unroll
     for (int t = 0; t < XL; ++t) {
-      const int e = tid + 256 * t, r = e / (kBD / 4), c4 = e % (kBD / 4);
-      const int64_t n = n0 + r;
-      xv[t] = (n < N && 4 * c4 < dn) ? *reinterpret_cast<const float4*>(x + n * D + d0 + 4 * c4)
-                                     : float4{0.f, 0.f, 0.f, 0.f};
+      const int c4 = (tid + 256 * t) % (kBD / 4);
+      xv[t] = (xrow[t] != nullptr && 4 * c4 < dn) ? load4_row(src, xrow[t], d0 + 4 * c4)
+                                                   : float4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
     for (int t = 0; t < WL; ++t) {
@@ -1149,8 +1204,9 @@ extern "C" int spruce_gate_project(const float* x, const float* w, int64_t N, in
     const int64_t brows = (N + 16 * TR - 1) / (16 * TR);
     SPRUCE_REQUIRE(brows < ((int64_t)1 << 31) && P < ((int64_t)1 << 20) && D < ((int64_t)1 << 20),
                    "projection too large");
-    hipLaunchKernelGGL((project_block_kernel<TR, TC>), dim3((unsigned)brows, (unsigned)((P + 16 * TC - 1) / (16 * TC))),
-                       dim3(256), 0, (hipStream_t)stream, x, w, N, (int)D, (int)P, out);
+    hipLaunchKernelGGL((project_block_kernel<TR, TC, ProjRowsF32>),
+                       dim3((unsigned)brows, (unsigned)((P + 16 * TC - 1) / (16 * TC))), dim3(256), 0,
+                       (hipStream_t)stream, ProjRowsF32{x}, w, N, (int)D, (int)P, out);
     return check_launch("project_block_kernel");
   }
   if (vec) {
@@ -1168,6 +1224,52 @@ extern "C" int spruce_gate_project(const float* x, const float* w, int64_t N, in
   hipLaunchKernelGGL(project_kernel, dim3((unsigned)rows, (unsigned)((P + kPC - 1) / kPC)), dim3(256), 0,
                      (hipStream_t)stream, x, w, N, (int)D, (int)P, out);
   return check_launch("project_kernel");
+}
+
+extern "C" int spruce_gate_project_levels(const void* const* levels, const int64_t* level_nodes, int64_t nlevels,
+                                          int64_t S, int64_t Pk, int64_t D, int dtype, const float* w, int64_t P,
+                                          float* out, void* stream) {
+  SPRUCE_REQUIRE(levels && level_nodes && w && out, "levels, level_nodes, w and out must be non-null");
+  SPRUCE_REQUIRE(nlevels >= 1 && nlevels <= kProjMaxSeg, "between 1 and %d levels, got %lld", kProjMaxSeg,
+                 (long long)nlevels);
+  SPRUCE_REQUIRE(S >= 1 && S < (1 << 20) && Pk >= 1 && Pk <= 1024 && D >= 4 && D <= 4096 && P >= 4 && P <= 4096,
+                 "invalid projection shape");
+  SPRUCE_REQUIRE(D % 4 == 0 && P % 4 == 0, "head_dim and projection dim must be multiples of 4");
+  SPRUCE_REQUIRE(dtype == SPRUCE_DTYPE_BF16 || dtype == SPRUCE_DTYPE_F16 || dtype == SPRUCE_DTYPE_F32,
+                 "unsupported dtype code %d", dtype);
+  const int eb = dtype == SPRUCE_DTYPE_F32 ? 4 : 2;
+  SPRUCE_REQUIRE(((uintptr_t)w % 16) == 0 && ((uintptr_t)out % 16) == 0, "w and out must be 16-byte aligned");
+  ProjSegs g{};
+  g.nseg = (int)nlevels;
+  g.P = (int)Pk;
+  int64_t total = 0;
+  for (int v = 0; v < nlevels; ++v) {
+    SPRUCE_REQUIRE(levels[v] != nullptr && level_nodes[v] >= 1 && level_nodes[v] < ((int64_t)1 << 30),
+                   "level %d: null buffer or node count out of range", v);
+    SPRUCE_REQUIRE(((uintptr_t)levels[v] % (size_t)(4 * eb)) == 0, "level %d is not %d-byte aligned", v, 4 * eb);
+    g.base[v] = levels[v];
+    g.off[v] = total;
+    total += level_nodes[v];
+  }
+  g.off[nlevels] = total;
+  g.N = total;
+  const int64_t N = S * total * Pk;
+  SPRUCE_REQUIRE(N * P < ((int64_t)1 << 40), "projection too large");
+  constexpr int TR = kBlockProjectTR, TC = kBlockProjectTC;
+  const int64_t brows = (N + 16 * TR - 1) / (16 * TR);
+  SPRUCE_REQUIRE(brows < ((int64_t)1 << 31), "projection too large");
+  const dim3 grid((unsigned)brows, (unsigned)((P + 16 * TC - 1) / (16 * TC)));
+  const hipStream_t st = (hipStream_t)stream;
+  if (dtype == SPRUCE_DTYPE_BF16)
+    hipLaunchKernelGGL((project_block_kernel<TR, TC, ProjRowsSeg<InBF16>>), grid, dim3(256), 0, st,
+                       ProjRowsSeg<InBF16>{g}, w, N, (int)D, (int)P, out);
+  else if (dtype == SPRUCE_DTYPE_F16)
+    hipLaunchKernelGGL((project_block_kernel<TR, TC, ProjRowsSeg<InF16>>), grid, dim3(256), 0, st,
+                       ProjRowsSeg<InF16>{g}, w, N, (int)D, (int)P, out);
+  else
+    hipLaunchKernelGGL((project_block_kernel<TR, TC, ProjRowsSeg<InF32>>), grid, dim3(256), 0, st,
+                       ProjRowsSeg<InF32>{g}, w, N, (int)D, (int)P, out);
+  return check_launch("project_block_kernel");
 }
 
 // Both selector projections in one launch (32-row tiles: at the selector's

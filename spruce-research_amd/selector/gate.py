@@ -16,7 +16,7 @@ import torch
 import torch.nn as nn
 
 import spruce_hip
-from selector.select import gate_scores, project
+from selector.select import gate_scores, project, project_levels
 
 
 class FlatGate(nn.Module):
@@ -36,9 +36,31 @@ class FlatGate(nn.Module):
 
     @staticmethod
     def _project(feat, W):
+        """``[L, ..., d] -> [L, ..., p]`` float32; 16-bit features are read as they
+        are (widened exactly in the kernel), float32 ones directly."""
+        def one(x, w):
+            if x.dtype in (torch.bfloat16, torch.float16) and x.shape[-1] % 4 == 0 and w.shape[-1] % 4 == 0:
+                rows = x.reshape(1, -1, 1, x.shape[-1])
+                return project_levels([rows], w).reshape(x.shape[:-1] + (w.shape[-1],))
+            return project(x.float(), w.float())
         if feat.shape[0] == 1:
-            return project(feat[0].float(), W[0].float()).unsqueeze(0)
-        return torch.stack([project(feat[l].float(), W[l].float()) for l in range(feat.shape[0])])
+            return one(feat[0], W[0]).unsqueeze(0)
+        return torch.stack([one(feat[l], W[l]) for l in range(feat.shape[0])])
+
+    @torch.no_grad()
+    def project_key_levels(self, level_features):
+        """Projects the levels of a key tree (each ``[L,G,n_v,P,d]``) into one
+        table ``[L,G,sum n_v,P,p]`` with node IDs leaf-first: the values of
+        ``project_keys(torch.cat(level_features, dim=2))`` without the copy."""
+        first = level_features[0]
+        L, G, _, P, d = first.shape
+        if first.dtype not in (torch.bfloat16, torch.float16, torch.float32) or d % 4 or self.proj_dim % 4:
+            return self.project_keys(torch.cat(level_features, dim=2))
+        outs = []
+        for l in range(L):
+            outs.append(project_levels([f[l] for f in level_features], self.Wk[l]))
+        out = outs[0].unsqueeze(0) if L == 1 else torch.stack(outs)
+        return out
 
     @torch.no_grad()
     def project_queries(self, q_feat):

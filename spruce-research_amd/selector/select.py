@@ -13,6 +13,7 @@ Shapes follow the reference: query ``[B,Hq,T,D]``, key ``[B,Hkv,T,D]`` (any
 strides with a contiguous last dim), gate weights ``[D, P]`` float32 (one
 layer of FlatGate's ``[L, d, p]``).
 """
+import ctypes
 import math
 
 import torch
@@ -81,6 +82,37 @@ def project(x, W):
             spruce_hip.ptr(x2), spruce_hip.ptr(W), N, D, P, spruce_hip.ptr(out), spruce_hip.stream_of(x))
     spruce_hip.check(rc, "spruce_gate_project")
     return out.reshape(x.shape[:-1] + (P,))
+
+
+def project_levels(levels, W):
+    """Projection of prototype rows kept in several buffers: ``levels`` is a
+    list of ``[S, n_v, P, D]`` tensors (bf16, f16 or float32, one dtype; the
+    levels of a key tree, leaf first) and the result is ``[S, sum n_v, P, p]``
+    float32, level after level along the node axis.  The same values as
+    ``project(torch.cat(levels, dim=1).float(), W)``, without the copies."""
+    if not levels:
+        raise ValueError("levels must not be empty")
+    for t in levels:
+        _cuda(t, "levels")
+    S, _, P, D = levels[0].shape
+    dtype = levels[0].dtype
+    for t in levels:
+        if t.dim() != 4 or t.shape[0] != S or t.shape[2:] != (P, D) or t.dtype != dtype:
+            raise ValueError("levels must be [S, n, P, D] with one S, P, D and dtype")
+    if W.dim() != 2 or W.shape[0] != D:
+        raise ValueError(f"shape mismatch: levels [..., {D}] @ W {tuple(W.shape)}")
+    W = W.to(device=levels[0].device, dtype=torch.float32).contiguous()
+    bufs = [t.contiguous() for t in levels]
+    nodes = [t.shape[1] for t in bufs]
+    out = torch.empty((S, sum(nodes), P, W.shape[1]), device=bufs[0].device, dtype=torch.float32)
+    ptrs = (ctypes.c_void_p * len(bufs))(*[t.data_ptr() for t in bufs])
+    counts = (ctypes.c_int64 * len(bufs))(*nodes)
+    with torch.cuda.device(bufs[0].device):
+        rc = spruce_hip.lib().spruce_gate_project_levels(
+            ptrs, counts, len(bufs), S, P, D, spruce_hip.dtype_code(bufs[0]), spruce_hip.ptr(W), W.shape[1],
+            spruce_hip.ptr(out), spruce_hip.stream_of(bufs[0]))
+    spruce_hip.check(rc, "spruce_gate_project_levels")
+    return out
 
 
 def project_pair(xa, Wa, xb, Wb):

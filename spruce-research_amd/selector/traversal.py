@@ -85,8 +85,10 @@ def traverse_to_leaf_ids(gate, q_feat, key_levels, beam, radix=2, layer_chunk=1)
     if not q_feat.is_cuda:
         raise RuntimeError("traverse_to_leaf_ids (HIP) requires GPU tensors")
     projected_q = gate.project_queries(q_feat)
-    features = torch.cat([lvl.features for lvl in key_levels], dim=2)
-    projected_k = gate.project_keys(features)
+    if hasattr(gate, "project_key_levels"):
+        projected_k = gate.project_key_levels([lvl.features for lvl in key_levels])
+    else:
+        projected_k = gate.project_keys(torch.cat([lvl.features for lvl in key_levels], dim=2))
     return traverse_projected(projected_q, projected_k, kb, beam, radix, math.sqrt(gate.proj_dim))
 
 

@@ -51,6 +51,8 @@ _SIGNATURES = {
         _p, _STRIDES, _p, _STRIDES, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _p, _p],
     "spruce_gate_project": [_p, _p, _i64, _i64, _i64, _p, _p],
     "spruce_gate_project2": [_p, _p, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _p],
+    "spruce_gate_project_levels": [ctypes.POINTER(_p), _STRIDES, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _i64,
+                                   _p, _p],
     "spruce_gate_scores": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int, _p, _p],
     "spruce_causal_topk": [_p, _i64, _i64, _i64, _i64, _p, _p],
     "spruce_teacher_block_mass": [

@@ -138,3 +138,20 @@ def test_noalloc_rejects_shapes_above_the_scratch_limit():
                                        fake, fake, fake, fake, None)
     assert rc == -1
     assert "above its limit" in spruce_hip.last_error()
+
+
+def test_project_levels_validation_before_launch():
+    lib = spruce_hip.lib()
+    fake = ctypes.c_void_p(1 << 20)
+    levels = (ctypes.c_void_p * 2)(fake, fake)
+    nodes = (ctypes.c_int64 * 2)(4, 2)
+    cases = [((levels, nodes, 0, 1, 8, 128, 0, fake, 128, fake, None), "between 1 and 32 levels"),
+             ((levels, nodes, 33, 1, 8, 128, 0, fake, 128, fake, None), "between 1 and 32 levels"),
+             ((levels, nodes, 2, 1, 8, 126, 0, fake, 128, fake, None), "multiples of 4"),
+             ((levels, nodes, 2, 1, 8, 128, 9, fake, 128, fake, None), "unsupported dtype"),
+             (((ctypes.c_void_p * 2)(fake, None), nodes, 2, 1, 8, 128, 0, fake, 128, fake, None), "level 1"),
+             (((ctypes.c_void_p * 2)(fake, ctypes.c_void_p((1 << 20) + 2)), nodes, 2, 1, 8, 128, 0, fake, 128,
+               fake, None), "not 8-byte aligned")]
+    for args, message in cases:
+        assert lib.spruce_gate_project_levels(*args) == -1, message
+        assert message in spruce_hip.last_error(), (message, spruce_hip.last_error())

@@ -103,6 +103,38 @@ def test_projection_pair_equals_single_launches(Na, Nb, D, P):
     assert torch.equal(oa, project(xa.to(DEV), Wa)) and torch.equal(ob, project(xb.to(DEV), Wb))
 
 
+@pytest.mark.parametrize("dtype,S,nodes,Pk,D,P", [
+    (torch.bfloat16, 4, [2048, 1024, 512, 256, 128, 64, 32, 16, 8, 4, 2, 1], 8, 128, 128),  # cfg5 key tree
+    (torch.float16, 3, [37, 19, 10, 5, 3, 2, 1], 4, 64, 36),   # ragged tiles, levels smaller than a tile
+    (torch.float32, 2, [100], 2, 96, 128),                      # one level (the query prototypes' use)
+    (torch.bfloat16, 1, [1, 1, 1], 1, 8, 4),                    # tiny levels and dims
+])
+def test_projection_of_levels_equals_projection_of_their_float_copy(dtype, S, nodes, Pk, D, P):
+    # spruce_gate_project_levels reads each level in the model dtype and
+    # widens it exactly: bit-identical to projecting a float32 copy of the
+    # concatenated levels, which the oracle pins.
+    from selector.select import project_levels
+    gen = torch.Generator().manual_seed(S + D + P + len(nodes))
+    levels = [torch.randn(S, n, Pk, D, generator=gen).to(dtype) for n in nodes]
+    W = torch.randn(D, P, generator=gen) * 0.1
+    got = project_levels([t.to(DEV) for t in levels], W.to(DEV))
+    flat = torch.cat(levels, dim=1).float()
+    assert got.shape == (S, sum(nodes), Pk, P)
+    assert torch.equal(got, project(flat.to(DEV), W))
+    if flat.numel() * P <= 1 << 24:
+        assert np.array_equal(_np(got).reshape(-1, P), osel.project(flat.reshape(-1, D).numpy(), W.numpy()))
+
+
+def test_flat_gate_key_levels_and_model_dtype_queries():
+    gen = torch.Generator().manual_seed(11)
+    gate = FlatGate(2, 64, proj_dim=32).to(DEV).eval()
+    q = torch.randn(2, 3, 40, 4, 64, generator=gen).to(torch.bfloat16).to(DEV)
+    levels = [torch.randn(2, 3, n, 4, 64, generator=gen).to(torch.bfloat16).to(DEV) for n in (40, 20, 10, 5, 3, 2, 1)]
+    with torch.no_grad():
+        assert torch.equal(gate.project_key_levels(levels), gate.project_keys(torch.cat(levels, dim=2).float()))
+        assert torch.equal(gate.project_queries(q), gate.project_queries(q.float()))
+
+
 @pytest.mark.parametrize("S,Qb,Pk,P", [
     (2, 130, 2, 128),    # triangular tile grid, ragged last tile
     (4, 1024, 2, 128),   # cfg3 score shape
