@@ -31,10 +31,12 @@ extern "C" {
 #define SPRUCE_OK 0
 #define SPRUCE_EINVAL (-1)
 
-/* Element type of Q/K/V and of the attention output. */
+/* Element type of Q/K/V and of the attention output (U8: boolean attention
+ * masks only, nonzero = attend). */
 #define SPRUCE_DTYPE_BF16 0
 #define SPRUCE_DTYPE_F16 1
 #define SPRUCE_DTYPE_F32 2
+#define SPRUCE_DTYPE_U8 3
 
 /* Kernel variants, in the order of the reference's KERNEL_VARIANTS tuple
  * (kernels/seerattention_direct_index_triton.py:17-23).  All variants compute
@@ -197,6 +199,29 @@ int spruce_sparse_prefill_index_masked(
     float scale, int dtype, int variant,
     void* out, const int64_t os[4],
     void* stream);
+
+/*
+ * The padded-list kernel with a general 4-D attention mask added to the
+ * scores, as sparse_prefill_attention_forward does with any Transformers
+ * mask (sparse/attention.py:223-229: scores scaled, future keys of the query
+ * masked, then + attention_mask[b, :, q, key] for every listed key).
+ *   amask  [B, Hm, Tq >= T, Tk >= T] with element strides ams (last 1),
+ *          Hm = 1 (broadcast over heads) or Hq (one mask per query head);
+ *   amask_dtype  SPRUCE_DTYPE_BF16 / F16 / F32: values added to the scaled
+ *          score (0 attends, -inf or finfo.min gives no weight); U8: boolean,
+ *          nonzero attends, zero gives no weight.
+ * A query row none of whose listed causal keys survives the mask writes
+ * zeros.  Same launch shapes and arithmetic as spruce_sparse_prefill_index
+ * otherwise.  No counterpart entry in the reference's kernels (its Triton
+ * callback rejects attention masks, kernels/sparse_prefill.py:73-79); this is
+ * the compute of its PyTorch path for masked prefill.
+ */
+int spruce_sparse_prefill_index_amask(const void* q, const int64_t qs[4], const void* k, const int64_t ks[4],
+                                      const void* v, const int64_t vs[4], const int32_t* idx, const int64_t is[4],
+                                      int64_t K, const void* amask, const int64_t ams[4], int64_t Hm,
+                                      int64_t Tq, int64_t Tk, int amask_dtype, int64_t B, int64_t Hq, int64_t Hkv,
+                                      int64_t T, int64_t D, float scale, int dtype, int variant, void* out,
+                                      const int64_t os[4], void* stream);
 
 /*
  * Residual-tree frontiers.  Replaces build_residual_summary_nodes /

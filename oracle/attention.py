@@ -25,6 +25,10 @@ Deliberate, documented choices where the reference has no single answer:
   * ``qblocks_subset`` computes only the listed query blocks (the others stay
     zero), so full-size configurations can be spot-checked row by row.
 
+``sparse_attention_index(add_mask=...)`` restates the additive 4-D mask of
+sparse/attention.py:225-229: the mask slice at the row's queries and listed
+keys is added to the scores after the causal fill.
+
 ``sparse_attention_summaries`` restates the residual-summary branch
 (sparse/attention.py:226-265): the row's exact keys plus, for each listed tree
 node and prototype with a non-zero count, the summary key with score
@@ -32,7 +36,10 @@ q . k / sqrt(D) + log(count) and the summary value, in one softmax.
 
 Pinned by tests/test_oracle_attention.py against the reference's own known
 answers (tests/test_sparse_attention.py:32-87 there), an independent dense
-closed form, a pure-Python brute force and structural invariants.
+closed form, a pure-Python brute force and structural invariants; the
+additive mask by the dense closed form with the same mask, the brute force
+with per-key biases, the key-padding path, and packed sequences that must
+equal each sequence attended alone.
 """
 import math
 
@@ -47,19 +54,28 @@ def _softmax_rows(s):
     return p / p.sum(axis=-1, keepdims=True)
 
 
-def _attend_group(qblk, keys, vals, q_pos, key_idx, scale, key_ok=None):
+def _attend_group(qblk, keys, vals, q_pos, key_idx, scale, key_ok=None, bias=None):
     """qblk [H, n, D], keys/vals [m, D] -> [H, n, D] (float32).  key_ok [m]:
-    key padding, scored finfo.min like the causal fill."""
+    key padding, scored finfo.min like the causal fill.  bias [H or 1, n, m]:
+    the additive mask slice, added after the causal fill
+    (sparse/attention.py:223-229); finfo.min + finfo.min overflows to -inf in
+    float32 there too.  A row whose every score is -inf is NaN, as the
+    reference's softmax makes it."""
     s = np.matmul(qblk, keys.T) * np.float32(scale) if scale is not None else \
         np.matmul(qblk, keys.T) / np.float32(math.sqrt(qblk.shape[-1]))
     causal = key_idx[None, :] <= q_pos[:, None]
     if key_ok is not None:
         causal = causal & key_ok[None, :]
     s = np.where(causal[None], s, F32_MIN)
-    return np.matmul(_softmax_rows(s), vals).astype(np.float32)
+    if bias is not None:
+        with np.errstate(over="ignore", invalid="ignore"):
+            s = (s + bias.astype(np.float32)).astype(np.float32)
+    with np.errstate(invalid="ignore"):
+        return np.matmul(_softmax_rows(s), vals).astype(np.float32)
 
 
-def _sparse_attention(q, k, v, blocks_for, block_size, scale, empty, qblocks_subset=None, key_valid=None):
+def _sparse_attention(q, k, v, blocks_for, block_size, scale, empty, qblocks_subset=None, key_valid=None,
+                      add_mask=None):
     q = np.asarray(q, dtype=np.float32)
     k = np.asarray(k, dtype=np.float32)
     v = np.asarray(v, dtype=np.float32)
@@ -93,24 +109,36 @@ def _sparse_attention(q, k, v, blocks_for, block_size, scale, empty, qblocks_sub
                     key_idx = (ids[:, None] * block_size + offs[None, :]).reshape(-1)
                     key_idx = key_idx[key_idx < T]
                     key_ok = None if key_valid is None else np.asarray(key_valid[b], dtype=bool)[key_idx]
+                    bias = None
+                    if add_mask is not None:
+                        mh = heads if add_mask.shape[1] > 1 else slice(0, 1)
+                        bias = add_mask[b, mh, q0:q1][..., key_idx]
                     out[b, heads, q0:q1] = _attend_group(
                         q[b, heads, q0:q1], k[b, g, key_idx], v[b, g, key_idx],
-                        q_pos, key_idx, scale, key_ok)
+                        q_pos, key_idx, scale, key_ok, bias)
     return out.transpose(0, 2, 1, 3).copy()
 
 
 def sparse_attention_index(q, k, v, idx, block_size=64, scale=None, empty="raise",
-                           qblocks_subset=None, key_valid=None):
+                           qblocks_subset=None, key_valid=None, add_mask=None):
     """Padded direct-index lists ``idx [B, Hkv, Qb, K]`` -> ``[B, T, Hq, D]``.
 
     key_valid: optional bool ``[B, T]`` key padding; padding keys get the
     finfo.min score of the reference's additive decoder mask
     (sparse/attention.py:225-229).  Rows at padding query positions whose
     listed causal keys are all padding are then a uniform average (the
-    reference's result too); callers compare real positions only."""
+    reference's result too); callers compare real positions only.
+
+    add_mask: optional additive mask ``[B, 1 or Hq, >=T, >=T]`` (float; -inf
+    allowed), whose slice at the row's queries and listed keys is added to
+    the scores after the causal fill, as sparse/attention.py:225-229 adds
+    ``attention_mask[b, :, q0:q1].index_select(-1, keys)``.  Mask head h goes
+    with query head h."""
     idx = np.asarray(idx)
+    if add_mask is not None:
+        add_mask = np.asarray(add_mask, dtype=np.float32)
     return _sparse_attention(q, k, v, lambda b, g, qb: idx[b, g, qb], block_size, scale, empty,
-                             qblocks_subset, key_valid)
+                             qblocks_subset, key_valid, add_mask)
 
 
 def sparse_attention_csr(q, k, v, indptr, indices, block_size=64, scale=None, empty="raise",
@@ -149,11 +177,12 @@ def sparse_attention_mask(q, k, v, mask, block_size=64, scale=None, empty="raise
     return _sparse_attention(q, k, v, blocks_for, block_size, scale, empty, qblocks_subset)
 
 
-def dense_causal_attention(q, k, v, scale=None):
+def dense_causal_attention(q, k, v, scale=None, add_mask=None):
     """Closed form: full [T, T] causal softmax attention, GQA by head repetition.
 
     Independent of the block gather above; used to pin it (all causal blocks
-    selected must reproduce this)."""
+    selected must reproduce this).  add_mask ``[B, 1 or Hq, T, T]`` is added
+    to the scaled scores (float64; -inf masks)."""
     q = np.asarray(q, dtype=np.float64)
     k = np.asarray(k, dtype=np.float64)
     v = np.asarray(v, dtype=np.float64)
@@ -164,17 +193,20 @@ def dense_causal_attention(q, k, v, scale=None):
     s = np.matmul(q, kr.transpose(0, 1, 3, 2)) * (scale if scale is not None else 1.0 / math.sqrt(D))
     future = np.triu(np.ones((T, T), dtype=bool), k=1)
     s = np.where(future[None, None], -np.inf, s)
+    if add_mask is not None:
+        s = s + np.asarray(add_mask, dtype=np.float64)[:, :, :T, :T]
     s = s - s.max(axis=-1, keepdims=True)
     p = np.exp(s)
     p /= p.sum(axis=-1, keepdims=True)
     return np.matmul(p, vr).transpose(0, 2, 1, 3)
 
 
-def attention_bruteforce(q, k, v, key_sets, scale=None):
+def attention_bruteforce(q, k, v, key_sets, scale=None, bias=None):
     """Pure-Python loops (math.exp, no numpy reductions) for tiny inputs.
 
     key_sets(b, hq, t) -> iterable of key token indices attended by query t of
-    query head hq.  Returns nested lists [B][T][Hq][D]."""
+    query head hq; bias(b, hq, t, j) -> finite number added to key j's score.
+    Returns nested lists [B][T][Hq][D]."""
     q = np.asarray(q, dtype=np.float64).tolist()
     k = np.asarray(k, dtype=np.float64).tolist()
     v = np.asarray(v, dtype=np.float64).tolist()
@@ -187,7 +219,8 @@ def attention_bruteforce(q, k, v, key_sets, scale=None):
             g = h // G
             for t in range(T):
                 keys = list(key_sets(b, h, t))
-                scores = [sum(q[b][h][t][d] * k[b][g][j][d] for d in range(D)) * sc for j in keys]
+                scores = [sum(q[b][h][t][d] * k[b][g][j][d] for d in range(D)) * sc
+                          + (bias(b, h, t, j) if bias is not None else 0.0) for j in keys]
                 mx = max(scores)
                 w = [math.exp(s - mx) for s in scores]
                 z = sum(w)

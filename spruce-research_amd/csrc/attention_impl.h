@@ -76,6 +76,16 @@ struct AttnParams {
   // real key token; padding keys get no weight.
   const uint8_t* kvalid;
   int64_t kvs;
+  // general 4-D attention mask (padded-list form only,
+  // sparse/attention.py:225-229): element strides ams over [B, Hm, Tq, Tk]
+  // (the last one 1), Hm = 1 or Hq; dtype bf16 / f16 / f32 (added to the
+  // scaled score) or u8 (bool: nonzero attends, zero gives no weight).
+  // amask_mul = log2(e) / cs turns a mask value into raw score units;
+  // amask_vec: 4-element groups may be read as one aligned load.
+  const void* amask;
+  int64_t ams[4];
+  int amask_dtype, amask_heads, amask_vec;
+  float amask_mul;
   // residual summaries (sparse/attention.py:226-265): per row, nodes
   // [B, Hkv, Qb, S] int32 (-1 = none); table keys/values float32
   // [B, Hkv, N, P, D] and natural-log counts [B, N, P], all contiguous.
@@ -477,12 +487,52 @@ constexpr int kSchedDsRead = 0x100;
 // K k-steps (two reads each; the V^T loop keeps the same number of reads).
 constexpr int kLookahead = 2;
 
+// Four mask values of one row at element el (keys el .. el + 3, of which the
+// first nvalid exist), as float: bool masks give 0 (attend) or -inf.
+__device__ __forceinline__ void amask_load4(const AttnParams& p, int64_t el, int nvalid, float (&v)[4]) {
+  const int dt = p.amask_dtype;
+  if (p.amask_vec && nvalid >= 4) {
+    if (dt == SPRUCE_DTYPE_F32) {
+      const float4 x = *reinterpret_cast<const float4*>(static_cast<const float*>(p.amask) + el);
+      v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+    } else if (dt == SPRUCE_DTYPE_U8) {
+      const uint32_t x = *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.amask) + el);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) v[t] = ((x >> (8 * t)) & 0xffu) ? 0.f : -INFINITY;
+    } else {
+      const uint2 x = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.amask) + el);
+      const bool f16 = dt == SPRUCE_DTYPE_F16;
+      v[0] = f16 ? unpack1<true>(x.x & 0xffffu) : unpack1<false>(x.x & 0xffffu);
+      v[1] = f16 ? unpack1<true>(x.x >> 16) : unpack1<false>(x.x >> 16);
+      v[2] = f16 ? unpack1<true>(x.y & 0xffffu) : unpack1<false>(x.y & 0xffffu);
+      v[3] = f16 ? unpack1<true>(x.y >> 16) : unpack1<false>(x.y >> 16);
+    }
+    return;
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    v[t] = 0.f;
+    if (t < nvalid) {
+      if (dt == SPRUCE_DTYPE_F32) {
+        v[t] = static_cast<const float*>(p.amask)[el + t];
+      } else if (dt == SPRUCE_DTYPE_U8) {
+        v[t] = static_cast<const uint8_t*>(p.amask)[el + t] ? 0.f : -INFINITY;
+      } else {
+        const uint32_t x = static_cast<const uint16_t*>(p.amask)[el + t];
+        v[t] = dt == SPRUCE_DTYPE_F16 ? unpack1<true>(x) : unpack1<false>(x);
+      }
+    }
+  }
+}
+
 template <int D, int WAVES, typename TIn, bool F16, int MODE, bool SUMM = false, bool CAP = false, bool PROD = false,
-          bool KVAL = false>
+          bool KVAL = false, bool AMASK = false>
 __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnParams p) {
   static_assert(!CAP || (MODE == kModeCausal && !SUMM && TIn::bytes == 2),
                 "feature capture runs on the dense causal form in the model dtype");
   static_assert(!KVAL || MODE == kModePadded, "key padding is supported for padded block lists");
+  static_assert(!AMASK || (MODE == kModePadded && !SUMM && !KVAL && !CAP),
+                "the general attention mask is supported for padded block lists without summaries");
   static_assert(!PROD || (!SUMM && TIn::bytes == 2), "the producer form stages 16-bit K/V for key blocks only");
   constexpr int NTHR = WAVES * 64;
   constexpr int KSTR = D + 8;        // K tile row stride, 16-bit elements (16 B pad)
@@ -734,10 +784,43 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     sc0 = s0;
     sc1 = s1;
   };
+  // General attention mask: the 32 values this lane adds to its scores of a
+  // key block (register r of key tile c holds key 32c + 8(r/4) + 4(lane/32)
+  // + r%4 of query q0 + l32), loaded before the block's S^T MFMAs.
+  float am0[AMASK ? 16 : 1], am1[AMASK ? 16 : 1];
+  auto load_amask = [&](int blk) {
+    if constexpr (AMASK) {
+      const int qt = q0 + l32;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) am0[r] = am1[r] = 0.f;
+      if (qt < p.T) {
+        const int mh = p.amask_heads > 1 ? head : 0;
+        const int64_t row = (int64_t)b * p.ams[0] + (int64_t)mh * p.ams[1] + (int64_t)qt * p.ams[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int key0 = blk * kBlock + 32 * c + 8 * j + 4 * hl;
+            float v[4];
+            amask_load4(p, row + key0, p.T - key0, v);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) (c == 0 ? am0 : am1)[4 * j + t] = v[t];
+          }
+      }
+    }
+  };
   // sb: per-key score bias of a summary chunk (null for a key block).
   // vb: validity bits of the block's 64 keys (key padding; all set otherwise).
   auto softmax = [&](bool diag, const float* sb, uint64_t vb) {
     f32x16_t s0 = sc0, s1 = sc1;
+    if constexpr (AMASK) {
+      // Added in raw score units: (s + mask * log2(e) / cs) * cs.
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s0[r] += am0[r] * p.amask_mul;
+        s1[r] += am1[r] * p.amask_mul;
+      }
+    }
     if constexpr (KVAL) {
       // Register r of key tile c holds key 32c + 8(r/4) + 4(lane/32) + r%4.
 #pragma unroll
@@ -780,7 +863,7 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
       const float m_new = fmaxf(m_use, cand);
       // With key padding a padded query row can still have no usable key
       // while others in the wave do: keep its (empty) state as it is.
-      const float alpha = (KVAL && m_new == -INFINITY) ? 1.f : fast_exp2(m_use - m_new);
+      const float alpha = ((KVAL || AMASK) && m_new == -INFINITY) ? 1.f : fast_exp2(m_use - m_new);
       m_use = m_new;
       l_run *= alpha;
 #pragma unroll
@@ -790,7 +873,7 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     }
     // A lane whose keys so far are all -inf (a summary-only row) keeps
     // m_use = -inf; exp2(-inf) = 0 needs a finite offset there.
-    const float nm = ((KVAL || sb != nullptr) && m_use == -INFINITY) ? 0.f : -m_use;
+    const float nm = ((KVAL || AMASK || sb != nullptr) && m_use == -INFINITY) ? 0.f : -m_use;
     float psum = 0.f;
 #pragma unroll
     for (int h2 = 0; h2 < 2; ++h2) {
@@ -834,8 +917,9 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
       acc[dt] = mfma32x32x16<F16>(va[i], pk[c][h2], acc[dt]);
     }
   };
-  auto compute = [&](int buf, bool diag, const float* sb, uint64_t vb) {
+  auto compute = [&](int buf, bool diag, const float* sb, uint64_t vb, int blk) {
     const uint16_t* Ks = smem + buf * BUF;
+    load_amask(blk);
     scores(Ks);
     softmax(diag, sb, vb);
     pv(Ks + KTILE);
@@ -881,7 +965,7 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
           bool nen = false;
           const bool more = it.next(nid, nen);
           const uint32_t vnext = more ? vbyte(nid) : 0u;
-          if (active && cur_en) compute(buf, cur_id == qb, nullptr, vbits(vcur));
+          if (active && cur_en) compute(buf, cur_id == qb, nullptr, vbits(vcur), cur_id);
           if (!more) break;
           __syncthreads();
           buf ^= 1;
@@ -902,7 +986,7 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
         const bool more = it.next(nid, nen);
         const uint32_t vnext = more ? vbyte(nid) : 0u;
         if (more) load_block(nid);
-        if (active && cur_en) compute(buf, cur_id == qb, nullptr, vbits(vcur));
+        if (active && cur_en) compute(buf, cur_id == qb, nullptr, vbits(vcur), cur_id);
         if (!more) break;
         store_block(buf ^ 1);
         __syncthreads();
@@ -968,7 +1052,7 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
         sbias[buf][tid] = node < 0 ? -INFINITY : p.slog[((int64_t)b * p.N + node) * p.P + en % p.P] * p.sbias;
       }
       __syncthreads();
-      if (active) compute(buf, false, sbias[buf], ~0ull);
+      if (active) compute(buf, false, sbias[buf], ~0ull, -1);
     }
   }
 
@@ -1095,40 +1179,41 @@ inline LaunchShape choose_shape(int variant, int G) {
 }
 
 template <int D, int WAVES, typename TIn, bool F16, int MODE, bool SUMM, bool CAP = false, bool PROD = false,
-          bool KVAL = false>
+          bool KVAL = false, bool AMASK = false>
 int launch_attention_t(const AttnParams& p, hipStream_t stream) {
   // Rows are padded to a multiple of the 8 XCDs; the extra workgroups exit.
   const int64_t rows8 = ((int64_t)p.B * p.Hkv * p.Qb + 7) / 8 * 8;
   const int64_t grid = rows8 * p.parts;
-  hipLaunchKernelGGL((sparse_prefill_kernel<D, WAVES, TIn, F16, MODE, SUMM, CAP, PROD, KVAL>), dim3((unsigned)grid),
-                     dim3(WAVES * 64), 0, stream, p);
+  hipLaunchKernelGGL((sparse_prefill_kernel<D, WAVES, TIn, F16, MODE, SUMM, CAP, PROD, KVAL, AMASK>),
+                     dim3((unsigned)grid), dim3(WAVES * 64), 0, stream, p);
   return check_launch("sparse_prefill_kernel");
 }
 
-template <int MODE, bool SUMM, int D, typename TIn, bool F16, bool KVAL>
+template <int MODE, bool SUMM, int D, typename TIn, bool F16, bool KVAL, bool AMASK = false>
 int launch_attention_w(const AttnParams& p, int waves, hipStream_t stream) {
   switch (waves) {
-    case 2: return launch_attention_t<D, 2, TIn, F16, MODE, SUMM, false, false, KVAL>(p, stream);
-    case 4: return launch_attention_t<D, 4, TIn, F16, MODE, SUMM, false, false, KVAL>(p, stream);
+    case 2: return launch_attention_t<D, 2, TIn, F16, MODE, SUMM, false, false, KVAL, AMASK>(p, stream);
+    case 4: return launch_attention_t<D, 4, TIn, F16, MODE, SUMM, false, false, KVAL, AMASK>(p, stream);
     case 8:
       // A spare wave becomes the K/V producer (16-bit inputs, key blocks only).
       if constexpr (kUseProducer && TIn::bytes == 2 && !SUMM)
-        if (p.tpp < 8) return launch_attention_t<D, 8, TIn, F16, MODE, SUMM, false, true, KVAL>(p, stream);
-      return launch_attention_t<D, 8, TIn, F16, MODE, SUMM, false, false, KVAL>(p, stream);
+        if (p.tpp < 8) return launch_attention_t<D, 8, TIn, F16, MODE, SUMM, false, true, KVAL, AMASK>(p, stream);
+      return launch_attention_t<D, 8, TIn, F16, MODE, SUMM, false, false, KVAL, AMASK>(p, stream);
     default: return set_error(SPRUCE_EINVAL, "unsupported wave count %d", waves);
   }
 }
 
-template <int MODE, bool SUMM = false, bool KVAL = false>
+template <int MODE, bool SUMM = false, bool KVAL = false, bool AMASK = false>
 int launch_attention(const AttnParams& p, int D, int dtype, int waves, hipStream_t stream) {
   if (D == 128) {
-    if (dtype == SPRUCE_DTYPE_BF16) return launch_attention_w<MODE, SUMM, 128, InBF16, false, KVAL>(p, waves, stream);
-    if (dtype == SPRUCE_DTYPE_F16) return launch_attention_w<MODE, SUMM, 128, InF16, true, KVAL>(p, waves, stream);
-    return launch_attention_w<MODE, SUMM, 128, InF32, false, KVAL>(p, waves, stream);
+    if (dtype == SPRUCE_DTYPE_BF16)
+      return launch_attention_w<MODE, SUMM, 128, InBF16, false, KVAL, AMASK>(p, waves, stream);
+    if (dtype == SPRUCE_DTYPE_F16) return launch_attention_w<MODE, SUMM, 128, InF16, true, KVAL, AMASK>(p, waves, stream);
+    return launch_attention_w<MODE, SUMM, 128, InF32, false, KVAL, AMASK>(p, waves, stream);
   }
-  if (dtype == SPRUCE_DTYPE_BF16) return launch_attention_w<MODE, SUMM, 64, InBF16, false, KVAL>(p, waves, stream);
-  if (dtype == SPRUCE_DTYPE_F16) return launch_attention_w<MODE, SUMM, 64, InF16, true, KVAL>(p, waves, stream);
-  return launch_attention_w<MODE, SUMM, 64, InF32, false, KVAL>(p, waves, stream);
+  if (dtype == SPRUCE_DTYPE_BF16) return launch_attention_w<MODE, SUMM, 64, InBF16, false, KVAL, AMASK>(p, waves, stream);
+  if (dtype == SPRUCE_DTYPE_F16) return launch_attention_w<MODE, SUMM, 64, InF16, true, KVAL, AMASK>(p, waves, stream);
+  return launch_attention_w<MODE, SUMM, 64, InF32, false, KVAL, AMASK>(p, waves, stream);
 }
 
 // Shared argument checks and parameter setup of the three entry points.

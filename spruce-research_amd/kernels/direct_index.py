@@ -62,13 +62,39 @@ def _key_valid(key_valid, B, T, device):
     return key_valid.to(torch.bool).contiguous().view(torch.uint8)
 
 
+_MASK_DTYPES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2, torch.bool: 3}
+
+
+def _attn_mask(mask, B, Hq, T, device):
+    """A 4-D attention mask ``[B, 1 or Hq, >=T, >=T]`` as (tensor, dtype code),
+    last dimension contiguous; bool stays bool (read as bytes), other float
+    types go to float32."""
+    if mask.dim() != 4:
+        raise ValueError(f"attn_mask must be 4-D [B, Hm, T, T], got {tuple(mask.shape)}")
+    if mask.shape[0] != B or mask.shape[1] not in (1, Hq) or mask.shape[2] < T or mask.shape[3] < T:
+        raise ValueError(f"attn_mask {tuple(mask.shape)} does not cover batch {B}, 1 or {Hq} heads and "
+                         f"{T} query/key tokens")
+    if mask.device != device:
+        raise ValueError("attn_mask must be on the same device as q")
+    if mask.dtype not in _MASK_DTYPES:
+        mask = mask.float()
+    if mask.stride(-1) != 1:
+        mask = mask.contiguous()
+    return mask, _MASK_DTYPES[mask.dtype]
+
+
 def direct_index_sparse_prefill(q, k, v, indices, scale, block_size=64,
-                                kernel_variant="single_head", key_valid=None):
+                                kernel_variant="single_head", key_valid=None, attn_mask=None):
     """Causal block-sparse attention over exactly the supplied block IDs.
 
     indices: int32 ``[B,Hkv,ceil(T/64),K]``; negative entries are padding.
     key_valid: optional bool ``[B,T]`` key padding (False keys get no weight;
     a query row with no valid causal listed key writes zeros).
+    attn_mask: optional 4-D mask ``[B, 1 or Hq, T, T]`` over (query, key)
+    tokens, added to the scaled scores of the listed causal keys as the
+    reference's PyTorch path does (sparse/attention.py:223-229): a float mask
+    is added (0 attends, -inf / finfo.min gives no weight), a bool mask
+    attends where True.  A query row with no surviving key writes zeros.
     Returns ``[B,T,Hq,D]`` in q's dtype.
     """
     B, Hq, Hkv, T, D = _check_common(q, k, v, block_size, kernel_variant)
@@ -82,6 +108,24 @@ def direct_index_sparse_prefill(q, k, v, indices, scale, block_size=64,
     if indices.device != q.device:
         raise ValueError("indices must be on the same device as q")
     out, out_strides = _output(q)
+    if attn_mask is not None:
+        if key_valid is not None:
+            raise ValueError("pass either key_valid or attn_mask, not both")
+        mask, code = _attn_mask(attn_mask, B, Hq, T, q.device)
+        mview = mask.view(torch.uint8) if mask.dtype == torch.bool else mask
+        with torch.cuda.device(q.device):
+            rc = spruce_hip.lib().spruce_sparse_prefill_index_amask(
+                spruce_hip.ptr(q), spruce_hip.strides(q),
+                spruce_hip.ptr(k), spruce_hip.strides(k),
+                spruce_hip.ptr(v), spruce_hip.strides(v),
+                spruce_hip.ptr(indices), spruce_hip.strides(indices), indices.shape[3],
+                spruce_hip.ptr(mview), spruce_hip.strides(mview), mask.shape[1], mask.shape[2], mask.shape[3],
+                code, B, Hq, Hkv, T, D, float(scale), spruce_hip.dtype_code(q),
+                spruce_hip.variant_code(kernel_variant),
+                spruce_hip.ptr(out), out_strides, spruce_hip.stream_of(q))
+        spruce_hip.check(rc, "spruce_sparse_prefill_index_amask")
+        _record(kernel_variant, Hq, Hkv, D)
+        return out
     if key_valid is not None:
         kv8 = _key_valid(key_valid, B, T, q.device)
         zero4 = spruce_hip.strides(torch.empty(0, 0, 0, 0))

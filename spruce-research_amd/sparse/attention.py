@@ -14,18 +14,23 @@ summary table of the layer's K/V is built on the GPU
 (``build_kv_summary_table``) and the same kernel appends one key per listed
 node and non-empty prototype, scored q.k/sqrt(D) + log(count).
 
-Padded batches (sparse/attention.py:147-150, 173-176, 225-229): a 4-D
-decoder mask -- boolean (True attends, Transformers' sdpa_mask) or additive
-(0 attends, -inf / finfo.min masks) -- is reduced to per-token key validity,
+Attention masks (sparse/attention.py:147-150, 173-176, 223-229): a 4-D
+decoder mask ``[B, 1 or Hq, T, T]`` -- boolean (True attends, Transformers'
+sdpa_mask) or additive (added to the scaled scores) -- takes one of two
+kernels.  When it is exactly "causal and key is a real token" at every real
+query position (padded batches), it is reduced to per-token key validity,
 which the kernel applies to every listed key block and which the residual
-summary table excludes.  The kernel applies causality itself, so the mask
-must be exactly "causal and key is a real token" at every real query
-position; any other pattern raises.  Outputs at padding query positions are
-not defined (a position with no real causal key writes zeros).
+summary table excludes.  Any other mask (block-diagonal packed sequences,
+score biases, per-head masks) is read by the kernel itself and added to the
+score of every listed causal key, as the reference adds its slice.  Outputs
+at query positions with no surviving key are not defined (the kernel writes
+zeros; the reference's softmax gives NaN there).
 
 Differences, all raising instead of computing something else:
   * ``block_size`` must be 64 and ``head_dim`` 64 or 128 (the kernel's tile);
-  * attention masks other than causal key padding (see above).
+  * residual summaries with a mask other than causal key padding.
+A boolean mask attends where True (Transformers' convention); the reference
+adds a boolean mask's 0/1 values to the scores like a float mask.
 """
 import math
 from typing import Optional
@@ -88,14 +93,7 @@ def _validate_inputs(query, key, value, selected_blocks, block_size, layer_idx, 
             f"for seq_len={query.shape[-2]} and block_size={block_size}")
 
 
-def _key_validity(attention_mask: torch.Tensor, batch: int, seq_len: int) -> torch.Tensor:
-    """The 4-D decoder mask as key validity ``[batch, seq_len]`` bool, after
-    checking that the mask is causal key padding at every real query position.
-
-    A key is real when the last query position attends it: in a causal
-    decoder mask that row sees every real key, with left or right padding,
-    and it is never a fully masked padding row that a mask builder may have
-    opened up to keep SDPA from producing NaN."""
+def _check_mask_shape(attention_mask: torch.Tensor, batch: int, heads: int, seq_len: int) -> None:
     if attention_mask.dim() != 4:
         raise ValueError(
             "Sparse prefill expects the Transformers 4D additive attention mask; "
@@ -104,28 +102,45 @@ def _key_validity(attention_mask: torch.Tensor, batch: int, seq_len: int) -> tor
         raise ValueError(
             f"attention mask {tuple(attention_mask.shape)} does not match batch {batch} and "
             f"{seq_len} query/key tokens")
+    if attention_mask.shape[1] not in (1, heads):
+        raise ValueError(
+            f"attention mask {tuple(attention_mask.shape)} must have 1 or {heads} heads")
+
+
+def _key_validity(attention_mask: torch.Tensor, batch: int, seq_len: int) -> Optional[torch.Tensor]:
+    """Key validity ``[batch, seq_len]`` bool when the 4-D decoder mask is
+    causal key padding (the same for every head, 0 / -inf or finfo.min
+    values, or bool); None for any other mask, which then goes to the kernel
+    as a general additive mask.
+
+    A key is real when the last query position attends it: in a causal
+    decoder mask that row sees every real key, with left or right padding,
+    and it is never a fully masked padding row that a mask builder may have
+    opened up to keep SDPA from producing NaN.  Every real query row must be
+    causal over the real keys; a padding query row may also attend nothing
+    or everything (Transformers opens fully masked rows up), but nothing
+    else, so packed sequences (a block-diagonal mask) are not taken for
+    left padding."""
     m = attention_mask
     if m.shape[1] != 1 and not bool((m == m[:, :1]).all()):
-        raise ValueError("per-head attention masks are not supported by the HIP sparse-prefill path")
+        return None
     m = m[:, 0]
     if m.dtype == torch.bool:
         attend = m
     else:
         attend = m >= 0
         if bool((m[attend] != 0).any()) or bool((m[~attend] > torch.finfo(m.dtype).min / 2).any()):
-            raise ValueError(
-                "additive attention masks must hold 0 (attend) or -inf / finfo.min (masked); "
-                "score biases are not supported by the HIP sparse-prefill path")
+            return None
     valid = attend[:, -1, :]
     keys = torch.arange(seq_len, device=m.device)
     for r0 in range(0, seq_len, 2048):
         r1 = min(r0 + 2048, seq_len)
+        rows = attend[:, r0:r1]
         expected = (keys[None, :] <= keys[r0:r1, None])[None] & valid[:, None, :]
-        wrong = (attend[:, r0:r1] != expected) & valid[:, r0:r1, None]
-        if bool(wrong.any()):
-            raise ValueError(
-                "the HIP sparse-prefill path applies causal attention with key padding only; "
-                "this attention mask has another pattern")
+        differs = (rows != expected).any(dim=-1)
+        opened = rows.all(dim=-1) | ~rows.any(dim=-1)
+        if bool((differs & (valid[:, r0:r1] | ~opened)).any()):
+            return None
     return valid
 
 
@@ -177,9 +192,17 @@ def sparse_prefill_attention_forward(
                 selected_blocks, residual_summary_nodes,
                 validate_selected=not validate_selected_blocks_input)
     key_valid = None
+    general_mask = None
     if attention_mask is not None:
+        _check_mask_shape(attention_mask, query.shape[0], query.shape[1], query.shape[-2])
         key_valid = _key_validity(attention_mask, query.shape[0], query.shape[-2])
-        if bool(key_valid.all()):
+        if key_valid is None:
+            if residual_summaries:
+                raise ValueError(
+                    "residual summaries on the HIP sparse-prefill path need a causal key-padding "
+                    "attention mask; this mask has another pattern")
+            general_mask = attention_mask   # added to the scores inside the kernel
+        elif bool(key_valid.all()):
             key_valid = None      # no padding: the plain kernel
     if block_size != 64:
         raise ValueError("the HIP sparse-prefill kernel requires block_size=64")
@@ -195,7 +218,7 @@ def sparse_prefill_attention_forward(
     if not residual_summaries:
         output = direct_index_sparse_prefill(
             query, key, value, indices, scale=1.0 / math.sqrt(D), block_size=block_size,
-            key_valid=key_valid)
+            key_valid=key_valid, attn_mask=general_mask)
         return output, None
     # Residual summaries (sparse/attention.py:163-182): the frontier nodes of
     # this layer, and the summary table of this layer's K/V over the tree.

@@ -155,3 +155,26 @@ def test_project_levels_validation_before_launch():
     for args, message in cases:
         assert lib.spruce_gate_project_levels(*args) == -1, message
         assert message in spruce_hip.last_error(), (message, spruce_hip.last_error())
+
+
+def test_attention_mask_validation_before_launch():
+    lib = spruce_hip.lib()
+    fake = ctypes.c_void_p(1 << 20)
+    st = _strides(0, 0, 128, 1)
+
+    def call(amask=fake, ams=(0, 0, 64, 1), Hm=1, Tq=64, Tk=64, code=2):
+        return lib.spruce_sparse_prefill_index_amask(
+            fake, st, fake, st, fake, st, fake, _strides(0, 0, 1, 1), 1,
+            amask, _strides(*ams), Hm, Tq, Tk, code, 1, 4, 2, 64, 128, 0.1, 0, 0,
+            fake, _strides(0, 128, 512, 1), None)
+
+    cases = [(dict(amask=None), "non-null"),
+             (dict(Hm=2), "1 or Hq"),
+             (dict(Tq=63), "must cover"),
+             (dict(Tk=32), "must cover"),
+             (dict(ams=(0, 0, 64, 2)), "contiguous last dimension"),
+             (dict(ams=(-64, 0, 64, 1)), "negative"),
+             (dict(code=7), "mask dtype")]
+    for kwargs, message in cases:
+        assert call(**kwargs) == -1, kwargs
+        assert message in spruce_hip.last_error(), (kwargs, spruce_hip.last_error())

@@ -214,3 +214,84 @@ def test_key_padding_matches_bruteforce_at_real_positions():
     np.testing.assert_array_equal(
         sparse_attention_index(q, k, v, idx, block_size=bs, key_valid=np.ones((B, T), bool)),
         sparse_attention_index(q, k, v, idx, block_size=bs))
+
+
+def test_additive_mask_all_causal_blocks_equal_dense_closed_form():
+    # sparse/attention.py:225-229 in the reference adds the mask slice to the
+    # scaled scores.  With every causal block listed this is dense attention
+    # with the same mask, computed in float64 by an independent closed form;
+    # per-head masks (mask head h with query head h) and -inf entries.
+    rng = np.random.default_rng(11)
+    B, Hq, Hkv, T, D, bs = 2, 4, 2, 10, 5, 4
+    q = rng.standard_normal((B, Hq, T, D)).astype(np.float32)
+    k = rng.standard_normal((B, Hkv, T, D)).astype(np.float32)
+    v = rng.standard_normal((B, Hkv, T, D)).astype(np.float32)
+    for Hm in (1, Hq):
+        mask = rng.standard_normal((B, Hm, T, T)).astype(np.float32) * 2
+        mask[rng.random(mask.shape) < 0.3] = -np.inf
+        diag = np.arange(T)
+        mask[:, :, diag, diag] = 0.0        # every row keeps its own key
+        out = sparse_attention_index(q, k, v, _all_causal(3, Hkv, B), block_size=bs,
+                                     add_mask=mask)
+        ref = dense_causal_attention(q, k, v, add_mask=mask)
+        np.testing.assert_allclose(out, ref, atol=2e-6, rtol=2e-5)
+
+
+def test_additive_mask_matches_bruteforce_with_messy_rows():
+    # Finite biases on listed keys, GQA, a ragged last block, unsorted rows
+    # with a duplicate and a future block: the mask is indexed by the listed
+    # key (not its position in the row) and by the query's own head.
+    rng = np.random.default_rng(12)
+    B, Hq, Hkv, T, D, bs = 1, 4, 2, 7, 3, 2
+    q = rng.standard_normal((B, Hq, T, D)).astype(np.float32)
+    k = rng.standard_normal((B, Hkv, T, D)).astype(np.float32)
+    v = rng.standard_normal((B, Hkv, T, D)).astype(np.float32)
+    mask = rng.standard_normal((B, Hq, T, T)).astype(np.float32)
+    idx = np.array([[[[0, -1, -1], [1, 0, 1], [2, 3, 0], [3, 1, -1]],
+                     [[0, 1, -1], [0, -1, -1], [1, 2, -1], [2, 3, 0]]]], np.int32)
+    out = sparse_attention_index(q, k, v, idx, block_size=bs, add_mask=mask)
+    ref = attention_bruteforce(q, k, v, _bruteforce_keys(lambda b, h, qb: idx[b, h // 2, qb], bs, T),
+                               bias=lambda b, h, t, j: float(mask[b, h, t, j]))
+    np.testing.assert_allclose(out, np.array(ref), atol=1e-5, rtol=1e-5)
+
+
+def test_additive_padding_mask_equals_key_padding():
+    # A 0 / finfo.min mask that is causal key padding gives the key-padding
+    # path's result at every real query position.
+    rng = np.random.default_rng(13)
+    B, Hq, Hkv, T, D, bs = 2, 2, 1, 9, 4, 4
+    q = rng.standard_normal((B, Hq, T, D)).astype(np.float32)
+    k = rng.standard_normal((B, Hkv, T, D)).astype(np.float32)
+    v = rng.standard_normal((B, Hkv, T, D)).astype(np.float32)
+    valid = np.zeros((B, T), bool)
+    valid[0, :6] = True
+    valid[1, 2:] = True
+    allowed = np.tril(np.ones((T, T), bool))[None] & valid[:, None, :]
+    mask = np.where(allowed, 0.0, np.finfo(np.float32).min).astype(np.float32)[:, None]
+    idx = _all_causal(3, Hkv, B)
+    by_mask = sparse_attention_index(q, k, v, idx, block_size=bs, add_mask=mask)
+    by_valid = sparse_attention_index(q, k, v, idx, block_size=bs, key_valid=valid)
+    np.testing.assert_allclose(by_mask[valid], by_valid[valid], atol=1e-6, rtol=1e-6)
+
+
+def test_packed_sequences_equal_each_sequence_alone():
+    # A block-diagonal mask over packed sequences: every sequence's output
+    # equals its attention computed alone (block-aligned starts, so the
+    # sequence's own blocks are a causal prefix of its own token range).
+    rng = np.random.default_rng(14)
+    Hq, Hkv, D, bs = 2, 1, 4, 4
+    lengths = [8, 5, 7]
+    starts = np.cumsum([0] + [8, 8])
+    T = int(starts[-1] + lengths[-1])
+    q = rng.standard_normal((1, Hq, T, D)).astype(np.float32)
+    k = rng.standard_normal((1, Hkv, T, D)).astype(np.float32)
+    v = rng.standard_normal((1, Hkv, T, D)).astype(np.float32)
+    seg = np.full(T, -1)
+    for i, (s0, n) in enumerate(zip(starts, lengths)):
+        seg[s0:s0 + n] = i
+    same = (seg[:, None] == seg[None, :]) & (seg[:, None] >= 0)
+    mask = np.where(same, 0.0, -np.inf).astype(np.float32)[None, None]
+    out = sparse_attention_index(q, k, v, _all_causal(-(-T // bs)), block_size=bs, add_mask=mask)
+    for s0, n in zip(starts, lengths):
+        alone = dense_causal_attention(q[:, :, s0:s0 + n], k[:, :, s0:s0 + n], v[:, :, s0:s0 + n])
+        np.testing.assert_allclose(out[:, s0:s0 + n], alone, atol=2e-6, rtol=2e-5)

@@ -2,11 +2,12 @@
 (sparse/attention.py:147-150,173-176,225-229 in the reference), on the CPU:
 boolean masks as Transformers' sdpa_mask builds them and additive masks as
 the eager path builds them, right and left padding; masks with any other
-pattern at a real query position are rejected."""
+pattern at a real query position give no key validity (they go to the
+kernel as a general mask), and malformed masks raise."""
 import pytest
 import torch
 
-from sparse.attention import _key_validity
+from sparse.attention import _check_mask_shape, _key_validity
 
 
 def _sdpa_style(lengths, T, left=False):
@@ -45,28 +46,57 @@ def test_padding_query_rows_are_not_constrained():
     assert torch.equal(_key_validity(mask, 1, 6), valid)
 
 
-@pytest.mark.parametrize("case", ["future_key", "missing_key", "bias", "per_head", "shape", "dims"])
-def test_other_mask_patterns_raise(case):
+def test_fully_masked_padding_rows_are_accepted():
+    # Left padding as sdpa_mask builds it: padding query rows attend nothing.
+    mask, valid = _sdpa_style([6, 3], 6, left=True)
+    assert not mask[1, 0, :3].any()
+    assert torch.equal(_key_validity(mask, 2, 6), valid)
+
+
+@pytest.mark.parametrize("case", ["future_key", "missing_key", "bias", "per_head", "packed",
+                                  "padding_row"])
+def test_other_mask_patterns_go_to_the_general_mask(case):
+    # Not causal key padding: no key validity, the kernel reads the mask itself.
     mask, _ = _sdpa_style([8, 6], 8)
     if case == "future_key":
         mask[0, 0, 3, 5] = True
-        match = "another pattern"
     elif case == "missing_key":
         mask[1, 0, 4, 2] = False
-        match = "another pattern"
     elif case == "bias":
         mask = torch.zeros(mask.shape).masked_fill(~mask, -1e9)
         mask[0, 0, 2, 1] = -0.5
-        match = "score biases"
     elif case == "per_head":
         mask = mask.expand(2, 2, 8, 8).clone()
         mask[0, 1, 5, 0] = False
-        match = "per-head"
-    elif case == "shape":
-        mask = mask[..., :7]
-        match = "does not match"
+    elif case == "packed":
+        # Sequences [0, 3) and [3, 8) packed into each row: the last query
+        # sees only the second, but the first is not padding.
+        seg = torch.tensor([0, 0, 0, 1, 1, 1, 1, 1])
+        mask = (torch.tril(torch.ones(8, 8, dtype=torch.bool)) & (seg[:, None] == seg[None, :]))
+        mask = mask[None, None].expand(2, 1, 8, 8)
     else:
-        mask = mask[:, 0]
-        match = "4D additive"
+        # A right-padding query row that attends one padding key.
+        mask[1, 0, 7, 6] = True
+        mask[1, 0, 7, 0] = False
+    _check_mask_shape(mask, 2, 2, 8)
+    assert _key_validity(mask, 2, 8) is None
+
+
+def test_per_head_copies_of_one_padding_mask_reduce_to_key_validity():
+    mask, valid = _sdpa_style([8, 6], 8)
+    assert torch.equal(_key_validity(mask.expand(2, 4, 8, 8), 2, 8), valid)
+
+
+@pytest.mark.parametrize("case", ["shape", "dims", "heads", "batch"])
+def test_malformed_masks_raise(case):
+    mask, _ = _sdpa_style([8, 6], 8)
+    if case == "shape":
+        mask, match = mask[..., :7], "does not match"
+    elif case == "dims":
+        mask, match = mask[:, 0], "4D additive"
+    elif case == "heads":
+        mask, match = mask.expand(2, 3, 8, 8), "1 or 4 heads"
+    else:
+        mask, match = mask[:1], "does not match"
     with pytest.raises(ValueError, match=match):
-        _key_validity(mask, 2, 8)
+        _check_mask_shape(mask, 2, 4, 8)
