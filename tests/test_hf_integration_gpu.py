@@ -214,6 +214,21 @@ def test_reference_acceptance_gate_at_qwen2_7b_attention_shape(backend, dtype):
           f"top10_overlap={lg['top10_overlap']:.2f}; final hidden relative_rmse={fh['relative_rmse']:.3e}",
           flush=True)
     assert result["accepted"], (lg, fh)
+    if dtype == torch.bfloat16:
+        # The margin that matters for bf16 weights: the same model with
+        # Transformers' own bf16 SDPA, against the same float32 dense run,
+        # is the noise floor of the deployed dtype.  The sparse kernel must
+        # stay near it (its extra error is P rounded to bf16, as in any
+        # bf16 flash kernel).  Measured: floor 1.460e-2, kernel 1.513e-2
+        # (ratio 1.036); the floor's top-10 set is unchanged, the kernel's
+        # differs in one near-tied token, the margin the 0.9 gate allows.
+        floor = run_equivalence(model, ids, dense_implementation=dense, sparse_implementation="sdpa")
+        flg, ffh = floor["logits"], floor["final_hidden"]
+        ratio = fh["relative_rmse"] / ffh["relative_rmse"]
+        print(f"bf16 SDPA floor: logits cosine={flg['cosine']:.6f} top10_overlap={flg['top10_overlap']:.2f}; "
+              f"final hidden relative_rmse={ffh['relative_rmse']:.3e}; kernel / floor = {ratio:.3f}",
+              flush=True)
+        assert ratio <= 1.15, (fh, ffh)
     if dtype == torch.float32:
         bound = 2.0 ** -8 * math.sqrt(cfg.num_hidden_layers)
         assert fh["relative_rmse"] <= bound and lg["top10_overlap"] == 1.0, (lg, fh, bound)
