@@ -319,7 +319,8 @@ def main():
                 return proto_pool_grouped(q5, Hkv, 64, 8), _proto_pool_seq(k5, 64, 8)
 
             def project(qf, levels):
-                return gate.project_queries(qf), gate.project_key_levels([lvl.features for lvl in levels])
+                return gate.project_queries(qf), gate.project_key_levels([lvl.features for lvl in levels],
+                                                                          interleaved=True)
 
             def route():
                 qf, kf = features()

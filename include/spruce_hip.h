@@ -38,6 +38,13 @@ extern "C" {
 #define SPRUCE_DTYPE_F32 2
 #define SPRUCE_DTYPE_U8 3
 
+/* Layouts of a projected key-prototype table of N nodes with Pk prototypes of
+ * P floats each: ROWS [N, Pk, P] (one prototype per row); INTERLEAVED
+ * [N, P/4, Pk, 4] (a node's prototypes interleaved by 4-float group, so the
+ * Pk prototypes' floats e..e+3 of one node are one contiguous 16*Pk bytes). */
+#define SPRUCE_KP_ROWS 0
+#define SPRUCE_KP_INTERLEAVED 1
+
 /* Kernel variants, in the order of the reference's KERNEL_VARIANTS tuple
  * (kernels/seerattention_direct_index_triton.py:17-23).  All variants compute
  * the same attention; they differ only in launch shape (and, for PRESCALE, in
@@ -288,7 +295,10 @@ int spruce_gate_project2(const float* xa, const float* wa, int64_t Na, const flo
  * [S, N, Pk, P] (N = sum of level_nodes) takes the levels' nodes in order
  * (node IDs leaf-first for a key tree).  Every value is widened to float32
  * exactly, so the results equal spruce_gate_project's on a float32 copy of
- * the concatenated levels.  Replaces FlatGate.project_keys over the levels of
+ * the concatenated levels.  layout SPRUCE_KP_ROWS writes out as above;
+ * SPRUCE_KP_INTERLEAVED writes [S, N, P/4, Pk, 4]: value (s, n, c, e) at
+ * ((s*N + n)*(P/4) + e/4)*Pk*4 + c*4 + e%4, the key layout
+ * spruce_tree_traverse reads fastest.  Replaces FlatGate.project_keys over the levels of
  * the key tree (selector/gate.py:124-127, called per level by
  * scripts/eval_tree_traversal.py:96) and, with one level,
  * FlatGate.project_queries (:120-122) on model-dtype prototypes.
@@ -296,7 +306,7 @@ int spruce_gate_project2(const float* xa, const float* wa, int64_t Na, const flo
  * buffers.
  */
 int spruce_gate_project_levels(const void* const* levels, const int64_t* level_nodes, int64_t nlevels, int64_t S,
-                               int64_t Pk, int64_t D, int dtype, const float* w, int64_t P, float* out,
+                               int64_t Pk, int64_t D, int dtype, const float* w, int64_t P, float* out, int layout,
                                void* stream);
 
 /*
@@ -369,10 +379,14 @@ int spruce_tree_merge_levels(const void* child, int64_t S, int64_t n, int64_t P,
  * spruce_gate_candidate_scores; a child is valid when it exists and its first
  * leaf is <= the query block.  beam*radix <= 64, Pq <= 16, Pk <= 64,
  * p % 4 == 0 and Pq*p <= 8192.  Node choices are bit-reproducible.
+ * layout: kp as SPRUCE_KP_ROWS (above) or SPRUCE_KP_INTERLEAVED
+ * ([S, N, p/4, Pk, 4], written by spruce_gate_project_levels); the results
+ * are identical, the interleaved table is read with 8x fewer cache lines per
+ * load instruction.
  */
 int spruce_tree_traverse(const float* qp, const float* kp, int64_t S, int64_t qb, int64_t kb, int64_t Pq,
                          int64_t Pk, int64_t p, int64_t radix, int64_t beam, float div, int32_t* out, int64_t C,
-                         void* stream);
+                         int layout, void* stream);
 
 /*
  * MaxSim scores of per-row candidate nodes.  Replaces

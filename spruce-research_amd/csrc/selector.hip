@@ -563,14 +563,20 @@ __device__ __forceinline__ float4 load4_row(const ProjRowsSeg<TIn>&, const void*
   }
 }
 
-template <int TR, int TC, typename Rows>
+// IL: rows are (node, prototype) pairs with ilk prototypes per node, and out
+// is [nodes, P/4, ilk, 4] (each node's prototypes interleaved by 4-column
+// group) instead of [N, P]; the output tile goes through LDS so that
+// neighbouring lanes store neighbouring 16-byte slots.
+template <int TR, int TC, typename Rows, bool IL = false>
 __global__ __launch_bounds__(256) void project_block_kernel(const Rows src, const float* __restrict__ w, int64_t N,
-                                                            int D, int P, float* __restrict__ out) {
+                                                            int D, int P, float* __restrict__ out, int ilk = 0) {
   constexpr int R = 16 * TR, C = 16 * TC;          // workgroup tile
   constexpr int XL = R * kBD / 4 / 256;            // x float4 per thread per slice
   constexpr int WL = C * kBD / 4 / 256;            // w float4 per thread per slice
-  __shared__ __attribute__((aligned(16))) float xs[kBD][R + 4];
-  __shared__ __attribute__((aligned(16))) float ws[kBD][C];
+  constexpr int kXs = kBD * (R + 4), kWs = kBD * C, kOut = IL ? R * (C + 4) : 0;
+  __shared__ __attribute__((aligned(16))) float smem[kXs + kWs > kOut ? kXs + kWs : kOut];
+  float (*xs)[R + 4] = reinterpret_cast<float (*)[R + 4]>(smem);
+  float (*ws)[C] = reinterpret_cast<float (*)[C]>(smem + kXs);
   const int tid = threadIdx.x;
   const int tr = tid >> 4, tc = tid & 15;
   const int64_t n0 = (int64_t)blockIdx.x * R;
@@ -643,15 +649,39 @@ __global__ __launch_bounds__(256) void project_block_kernel(const Rows src, cons
         for (int c = 0; c < TC; ++c) acc[a][c] = __builtin_fmaf(av[a], bv[c], acc[a][c]);
     }
   }
+  if constexpr (IL) {
+    // Tile [R][C + 4] in LDS, then slot s = (group g, row) with the row
+    // fastest: consecutive rows of a node are consecutive 16-byte slots of
+    // out (value (n, j) at node * ilk * P + (j / 4) * 4 * ilk + proto * 4).
+    constexpr int OS = C + 4;
+    __syncthreads();  // every read of xs / ws is done
 #pragma unroll
-  for (int a = 0; a < TR; ++a) {
-    const int64_t n = n0 + TR * tr + a;
-    if (n >= N) continue;
+    for (int a = 0; a < TR; ++a)
 #pragma unroll
-    for (int c = 0; c < TC; c += 4) {
-      const int j = j0 + TC * tc + c;
-      if (j < P)
-        *reinterpret_cast<float4*>(out + n * P + j) = float4{acc[a][c], acc[a][c + 1], acc[a][c + 2], acc[a][c + 3]};
+      for (int c = 0; c < TC; c += 4)
+        *reinterpret_cast<float4*>(&smem[(TR * tr + a) * OS + TC * tc + c]) =
+            float4{acc[a][c], acc[a][c + 1], acc[a][c + 2], acc[a][c + 3]};
+    __syncthreads();
+    for (int sl = tid; sl < R * (C / 4); sl += 256) {
+      const int row = sl % R, g = sl / R;
+      const int64_t n = n0 + row;
+      const int j = j0 + 4 * g;
+      if (n >= N || j >= P) continue;
+      const int64_t node = n / ilk;
+      *reinterpret_cast<float4*>(out + node * ilk * P + (int64_t)(j / 4) * 4 * ilk + (n - node * ilk) * 4) =
+          *reinterpret_cast<const float4*>(&smem[row * OS + 4 * g]);
+    }
+  } else {
+#pragma unroll
+    for (int a = 0; a < TR; ++a) {
+      const int64_t n = n0 + TR * tr + a;
+      if (n >= N) continue;
+#pragma unroll
+      for (int c = 0; c < TC; c += 4) {
+        const int j = j0 + TC * tc + c;
+        if (j < P)
+          *reinterpret_cast<float4*>(out + n * P + j) = float4{acc[a][c], acc[a][c + 1], acc[a][c + 2], acc[a][c + 3]};
+      }
     }
   }
 }
@@ -1228,8 +1258,9 @@ extern "C" int spruce_gate_project(const float* x, const float* w, int64_t N, in
 
 extern "C" int spruce_gate_project_levels(const void* const* levels, const int64_t* level_nodes, int64_t nlevels,
                                           int64_t S, int64_t Pk, int64_t D, int dtype, const float* w, int64_t P,
-                                          float* out, void* stream) {
+                                          float* out, int layout, void* stream) {
   SPRUCE_REQUIRE(levels && level_nodes && w && out, "levels, level_nodes, w and out must be non-null");
+  SPRUCE_REQUIRE(layout == SPRUCE_KP_ROWS || layout == SPRUCE_KP_INTERLEAVED, "unknown output layout %d", layout);
   SPRUCE_REQUIRE(nlevels >= 1 && nlevels <= kProjMaxSeg, "between 1 and %d levels, got %lld", kProjMaxSeg,
                  (long long)nlevels);
   SPRUCE_REQUIRE(S >= 1 && S < (1 << 20) && Pk >= 1 && Pk <= 1024 && D >= 4 && D <= 4096 && P >= 4 && P <= 4096,
@@ -1260,15 +1291,22 @@ extern "C" int spruce_gate_project_levels(const void* const* levels, const int64
   SPRUCE_REQUIRE(brows < ((int64_t)1 << 31), "projection too large");
   const dim3 grid((unsigned)brows, (unsigned)((P + 16 * TC - 1) / (16 * TC)));
   const hipStream_t st = (hipStream_t)stream;
+  const bool il = layout == SPRUCE_KP_INTERLEAVED;
+  auto go = [&](auto rows) {
+    using RowsT = decltype(rows);
+    if (il)
+      hipLaunchKernelGGL((project_block_kernel<TR, TC, RowsT, true>), grid, dim3(256), 0, st, rows, w, N, (int)D,
+                         (int)P, out, (int)Pk);
+    else
+      hipLaunchKernelGGL((project_block_kernel<TR, TC, RowsT, false>), grid, dim3(256), 0, st, rows, w, N, (int)D,
+                         (int)P, out, 0);
+  };
   if (dtype == SPRUCE_DTYPE_BF16)
-    hipLaunchKernelGGL((project_block_kernel<TR, TC, ProjRowsSeg<InBF16>>), grid, dim3(256), 0, st,
-                       ProjRowsSeg<InBF16>{g}, w, N, (int)D, (int)P, out);
+    go(ProjRowsSeg<InBF16>{g});
   else if (dtype == SPRUCE_DTYPE_F16)
-    hipLaunchKernelGGL((project_block_kernel<TR, TC, ProjRowsSeg<InF16>>), grid, dim3(256), 0, st,
-                       ProjRowsSeg<InF16>{g}, w, N, (int)D, (int)P, out);
+    go(ProjRowsSeg<InF16>{g});
   else
-    hipLaunchKernelGGL((project_block_kernel<TR, TC, ProjRowsSeg<InF32>>), grid, dim3(256), 0, st,
-                       ProjRowsSeg<InF32>{g}, w, N, (int)D, (int)P, out);
+    go(ProjRowsSeg<InF32>{g});
   return check_launch("project_block_kernel");
 }
 

@@ -219,23 +219,31 @@ __global__ __launch_bounds__(64 * kTopWaves) void tree_merge_top_kernel(const Me
 
 struct ScoreParams2 {
   const float* qp;  // [S, qb, Pq, p]
-  const float* kp;  // [S, N, Pk, p]
+  const float* kp;  // [S, N, Pk, p] (rows) or [S, N, p/4, Pk, 4] (interleaved)
   int64_t S;
   int qb, N, Pq, Pk, pd;
   float div;
+  int cstride;      // floats from a node's prototype c to c + 1: p (rows) or 4
+  int gs;           // floats from a prototype's 4-float group to the next: 4 or 4 * Pk
 };
+
+// Offset of prototype c of node `node` (counted from the table's start).
+__device__ __forceinline__ int64_t kvec(const ScoreParams2& sc, int64_t node, int c) {
+  return node * sc.Pk * (int64_t)sc.pd + (int64_t)c * sc.cstride;
+}
 
 // Max over query prototypes of q_a . k (fmaf chains over the projection dim,
 // all a at once; each chain runs e = 0..p-1 in order).  qrow in LDS.
-__device__ __forceinline__ float maxsim_one(const float* qrow, const float* krow, int Pq, int pd) {
+__device__ __forceinline__ float maxsim_one(const float* qrow, const float* krow, int Pq, int pd, int gs) {
   float acc[16];
 #pragma unroll
   for (int a = 0; a < 16; ++a) acc[a] = 0.f;
-  // The key vector streams from L2 one 64-byte line quarter ahead of its use.
+  // The key vector (4-float groups gs floats apart) streams from L2 one
+  // group ahead of its use.
   float4 knext = *reinterpret_cast<const float4*>(krow);
   for (int e = 0; e < pd; e += 4) {
     const float4 k4 = knext;
-    if (e + 4 < pd) knext = *reinterpret_cast<const float4*>(krow + e + 4);
+    if (e + 4 < pd) knext = *reinterpret_cast<const float4*>(krow + (int64_t)(e / 4 + 1) * gs);
 #pragma unroll
     for (int a = 0; a < 16; ++a) {
       if (a < Pq) {
@@ -260,53 +268,67 @@ __device__ __forceinline__ float maxsim_one(const float* qrow, const float* krow
 // of query prototypes: every query float4 read from LDS feeds all NP pairs,
 // and each chain is the same fmaf sequence as maxsim_one (e ascending), so
 // the results are identical.  The key vectors stream in pieces of CW float4
-// (loads back to back, the next piece in flight while the current one is
-// used): lanes read different vectors, and taking a line in a few pieces
-// close together keeps it in L1 between them, where one float4 per step was
-// refetched from L2 for every 16 bytes (measured 1.85 -> 1.0-1.1 ms at the
-// cfg5 grid).  Requires pd % (4 * CW) == 0.
-template <int PQ, int NP, int CW>
-__device__ __forceinline__ void maxsim_multi(const float* qrow, const float* const (&kv)[NP], int pd,
+// (loads back to back): lanes read different vectors, and taking a line in a
+// few pieces close together keeps it in L1 between them, where one float4
+// per step was refetched from L2 for every 16 bytes (measured 1.85 -> 1.0-1.1
+// ms at the cfg5 grid).  Two register sets take the pieces in turn, the next
+// piece loading while the other is used, so no piece is copied between
+// registers (the loads are unconditional: the last one re-reads piece 0,
+// in bounds and unused).  Requires pd % (8 * CW) == 0; PD > 0 fixes pd at
+// compile time, so the query reads take immediate LDS offsets, and GS > 0
+// the key group stride (4: rows layout; 4 * Pk: interleaved, where the Pk
+// prototypes of a node that neighbouring lanes hold share each 16 * Pk-byte
+// group, so a load touches one line per node instead of one per lane).
+template <int NP, int CW, int GS>
+__device__ __forceinline__ void load_piece(const float* const (&kv)[NP], int e0, int gs_rt, float4 (&k)[NP][CW]) {
+  const int gs = GS > 0 ? GS : gs_rt;
+#pragma unroll
+  for (int n = 0; n < NP; ++n)
+#pragma unroll
+    for (int j = 0; j < CW; ++j)
+      k[n][j] = *reinterpret_cast<const float4*>(kv[n] + (int64_t)(e0 / 4 + j) * gs);
+}
+
+template <int PQ, int NP, int CW, int PD>
+__device__ __forceinline__ void fma_piece(const float* qrow, int pd_rt, int e0, const float4 (&k)[NP][CW],
+                                          float (&acc)[NP][PQ]) {
+  const int pd = PD > 0 ? PD : pd_rt;
+#pragma unroll
+  for (int j = 0; j < CW; ++j) {
+    const int e = e0 + 4 * j;
+#pragma unroll
+    for (int a = 0; a < PQ; ++a) {
+      const float4 q4 = *reinterpret_cast<const float4*>(qrow + a * pd + e);
+#pragma unroll
+      for (int n = 0; n < NP; ++n) {
+        float t = acc[n][a];
+        t = fmaf(q4.x, k[n][j].x, t);
+        t = fmaf(q4.y, k[n][j].y, t);
+        t = fmaf(q4.z, k[n][j].z, t);
+        t = fmaf(q4.w, k[n][j].w, t);
+        acc[n][a] = t;
+      }
+    }
+  }
+}
+
+template <int PQ, int NP, int CW, int PD, int GS>
+__device__ __forceinline__ void maxsim_multi(const float* qrow, const float* const (&kv)[NP], int pd_rt, int gs,
                                              float (&res)[NP]) {
+  const int pd = PD > 0 ? PD : pd_rt;
   float acc[NP][PQ];
 #pragma unroll
   for (int n = 0; n < NP; ++n)
 #pragma unroll
     for (int a = 0; a < PQ; ++a) acc[n][a] = 0.f;
-  float4 nxt[NP][CW];
-#pragma unroll
-  for (int n = 0; n < NP; ++n)
-#pragma unroll
-    for (int j = 0; j < CW; ++j) nxt[n][j] = *reinterpret_cast<const float4*>(kv[n] + 4 * j);
-  for (int e0 = 0; e0 < pd; e0 += 4 * CW) {
-    float4 cur[NP][CW];
-#pragma unroll
-    for (int n = 0; n < NP; ++n)
-#pragma unroll
-      for (int j = 0; j < CW; ++j) cur[n][j] = nxt[n][j];
-    if (e0 + 4 * CW < pd) {
-#pragma unroll
-      for (int n = 0; n < NP; ++n)
-#pragma unroll
-        for (int j = 0; j < CW; ++j) nxt[n][j] = *reinterpret_cast<const float4*>(kv[n] + e0 + 4 * CW + 4 * j);
-    }
-#pragma unroll
-    for (int j = 0; j < CW; ++j) {
-      const int e = e0 + 4 * j;
-#pragma unroll
-      for (int a = 0; a < PQ; ++a) {
-        const float4 q4 = *reinterpret_cast<const float4*>(qrow + a * pd + e);
-#pragma unroll
-        for (int n = 0; n < NP; ++n) {
-          float t = acc[n][a];
-          t = fmaf(q4.x, cur[n][j].x, t);
-          t = fmaf(q4.y, cur[n][j].y, t);
-          t = fmaf(q4.z, cur[n][j].z, t);
-          t = fmaf(q4.w, cur[n][j].w, t);
-          acc[n][a] = t;
-        }
-      }
-    }
+  constexpr int kStep = 4 * CW;
+  float4 ka[NP][CW], kb[NP][CW];
+  load_piece<NP, CW, GS>(kv, 0, gs, ka);
+  for (int e0 = 0; e0 < pd; e0 += 2 * kStep) {
+    load_piece<NP, CW, GS>(kv, e0 + kStep, gs, kb);
+    fma_piece<PQ, NP, CW, PD>(qrow, pd, e0, ka, acc);
+    load_piece<NP, CW, GS>(kv, e0 + 2 * kStep < pd ? e0 + 2 * kStep : 0, gs, ka);
+    fma_piece<PQ, NP, CW, PD>(qrow, pd, e0 + kStep, kb, acc);
   }
 #pragma unroll
   for (int n = 0; n < NP; ++n) {
@@ -335,7 +357,7 @@ struct TraverseParams {
 // Scores pairs pr + 64 n (n < NP) of one level into pm.  An invalid or
 // missing pair reads the level's first node (always in range) and its result
 // is dropped.
-template <int PQ, int NP>
+template <int PQ, int NP, int PD, int GS>
 __device__ __forceinline__ void score_pairs(const ScoreParams2& sc, const float* qrow, const float* kl,
                                             const int* cand, const int* valid, int npairs, int lane,
                                             float* pm) {
@@ -349,10 +371,10 @@ __device__ __forceinline__ void score_pairs(const ScoreParams2& sc, const float*
       idx[n] = pn < npairs ? pn / sc.Pk : 0;
       cc[n] = pn < npairs ? pn - idx[n] * sc.Pk : 0;
       ok[n] = pn < npairs && valid[idx[n]] != 0;
-      kv[n] = kl + (ok[n] ? ((int64_t)cand[idx[n]] * sc.Pk + cc[n]) * sc.pd : 0);
+      kv[n] = kl + (ok[n] ? kvec(sc, cand[idx[n]], cc[n]) : 0);
     }
     float m[NP];
-    maxsim_multi<PQ, NP, kTravCW>(qrow, kv, sc.pd, m);
+    maxsim_multi<PQ, NP, kTravCW, PD, GS>(qrow, kv, sc.pd, sc.gs, m);
 #pragma unroll
     for (int n = 0; n < NP; ++n)
       if (pr + 64 * n < npairs) pm[idx[n] * sc.Pk + cc[n]] = ok[n] ? m[n] : 0.f;
@@ -362,7 +384,7 @@ __device__ __forceinline__ void score_pairs(const ScoreParams2& sc, const float*
 // One wavefront per (slab, query block) row.  PQ > 0: that many query
 // prototypes, two pairs per lane per step (one on levels of at most 64
 // pairs); PQ == 0: any count, one pair.
-template <int PQ>
+template <int PQ, int PD = 0, int GS = 0>
 __global__ __launch_bounds__(64) void tree_traverse_kernel(const TraverseParams p) {
   extern __shared__ float sh[];
   const ScoreParams2& sc = p.sc;
@@ -394,18 +416,18 @@ __global__ __launch_bounds__(64) void tree_traverse_kernel(const TraverseParams 
     __syncthreads();
     const float* kl = sc.kp + (s * sc.N + p.offset[v]) * (int64_t)sc.Pk * sc.pd;
     const int npairs = ncand * sc.Pk;
-    if (PQ > 0 && sc.pd % (4 * kTravCW) == 0) {
+    if (PQ > 0 && sc.pd % (8 * kTravCW) == 0) {
       // A level with at most 64 pairs (the tree's top levels) takes one pair
       // per lane: with two, half of every lane's chains would be dropped.
       if (npairs <= 64)
-        score_pairs<PQ == 0 ? 1 : PQ, 1>(sc, qrow, kl, cand, valid, npairs, lane, pm);
+        score_pairs<PQ == 0 ? 1 : PQ, 1, PD, GS>(sc, qrow, kl, cand, valid, npairs, lane, pm);
       else
-        score_pairs<PQ == 0 ? 1 : PQ, kTravNP>(sc, qrow, kl, cand, valid, npairs, lane, pm);
+        score_pairs<PQ == 0 ? 1 : PQ, kTravNP, PD, GS>(sc, qrow, kl, cand, valid, npairs, lane, pm);
     } else {
       for (int pr = lane; pr < npairs; pr += 64) {
         const int i = pr / sc.Pk, c = pr - (pr / sc.Pk) * sc.Pk;
         float m = 0.f;
-        if (valid[i]) m = maxsim_one(qrow, kl + ((int64_t)cand[i] * sc.Pk + c) * sc.pd, sc.Pq, sc.pd);
+        if (valid[i]) m = maxsim_one(qrow, kl + kvec(sc, cand[i], c), sc.Pq, sc.pd, sc.gs);
         pm[i * sc.Pk + c] = m;
       }
     }
@@ -469,7 +491,7 @@ __global__ __launch_bounds__(64) void candidate_scores_kernel(const CandParams p
       const int i = pr / sc.Pk, c = pr - (pr / sc.Pk) * sc.Pk;
       int node = idr[c0 + i];
       node = node < 0 ? 0 : (node >= sc.N ? sc.N - 1 : node);  // clamped like the reference
-      pm[i * sc.Pk + c] = maxsim_one(qrow, sc.kp + ((s * sc.N + node) * sc.Pk + c) * (int64_t)sc.pd, sc.Pq, sc.pd);
+      pm[i * sc.Pk + c] = maxsim_one(qrow, sc.kp + kvec(sc, s * sc.N + node, c), sc.Pq, sc.pd, sc.gs);
     }
     __syncthreads();
     if (lane < nc) {
@@ -586,8 +608,9 @@ extern "C" int spruce_tree_merge_levels(const void* child, int64_t S, int64_t n,
 
 extern "C" int spruce_tree_traverse(const float* qp, const float* kp, int64_t S, int64_t qb, int64_t kb, int64_t Pq,
                                     int64_t Pk, int64_t pd, int64_t radix, int64_t beam, float div, int32_t* out,
-                                    int64_t C, void* stream) {
+                                    int64_t C, int layout, void* stream) {
   SPRUCE_REQUIRE(out != nullptr, "out must be a non-null device pointer");
+  SPRUCE_REQUIRE(layout == SPRUCE_KP_ROWS || layout == SPRUCE_KP_INTERLEAVED, "unknown key table layout %d", layout);
   SPRUCE_REQUIRE(kb >= 1 && kb < ((int64_t)1 << 30), "key blocks must be in [1, 2^30)");
   SPRUCE_REQUIRE(radix >= 2, "radix must be >= 2, got %lld", (long long)radix);
   SPRUCE_REQUIRE(beam >= 1, "beam must be >= 1, got %lld", (long long)beam);
@@ -617,7 +640,9 @@ extern "C" int spruce_tree_traverse(const float* qp, const float* kp, int64_t S,
     W = k < p.count[v] ? k : p.count[v];
   }
   SPRUCE_REQUIRE(C == W, "out width must be %lld for this tree and beam, got %lld", (long long)W, (long long)C);
-  p.sc = ScoreParams2{qp, kp, S, (int)qb, (int)total, (int)Pq, (int)Pk, (int)pd, div};
+  const bool il = layout == SPRUCE_KP_INTERLEAVED;
+  p.sc = ScoreParams2{qp, kp, S, (int)qb, (int)total, (int)Pq, (int)Pk, (int)pd, div, il ? 4 : (int)pd,
+                      il ? 4 * (int)Pk : 4};
   p.kb = (int)kb;
   p.radix = (int)radix;
   p.beam = (int)beam;
@@ -630,7 +655,15 @@ extern "C" int spruce_tree_traverse(const float* qp, const float* kp, int64_t S,
     case 1: hipLaunchKernelGGL(tree_traverse_kernel<1>, grid, dim3(64), lds, (hipStream_t)stream, p); break;
     case 2: hipLaunchKernelGGL(tree_traverse_kernel<2>, grid, dim3(64), lds, (hipStream_t)stream, p); break;
     case 4: hipLaunchKernelGGL(tree_traverse_kernel<4>, grid, dim3(64), lds, (hipStream_t)stream, p); break;
-    case 8: hipLaunchKernelGGL(tree_traverse_kernel<8>, grid, dim3(64), lds, (hipStream_t)stream, p); break;
+    case 8:
+      // The deployed shape (8 prototypes, p = 128) with compile-time strides.
+      if (pd == 128 && il && Pk == 8)
+        hipLaunchKernelGGL((tree_traverse_kernel<8, 128, 32>), grid, dim3(64), lds, (hipStream_t)stream, p);
+      else if (pd == 128 && !il)
+        hipLaunchKernelGGL((tree_traverse_kernel<8, 128, 4>), grid, dim3(64), lds, (hipStream_t)stream, p);
+      else
+        hipLaunchKernelGGL(tree_traverse_kernel<8>, grid, dim3(64), lds, (hipStream_t)stream, p);
+      break;
     default: hipLaunchKernelGGL(tree_traverse_kernel<0>, grid, dim3(64), lds, (hipStream_t)stream, p); break;
   }
   return check_launch("tree_traverse_kernel");
@@ -643,7 +676,7 @@ extern "C" int spruce_gate_candidate_scores(const float* qp, const float* kp, co
   if (rc) return rc;
   SPRUCE_REQUIRE(C >= 1 && ids != nullptr && out != nullptr, "ids and out must be non-null with C >= 1");
   CandParams p{};
-  p.sc = ScoreParams2{qp, kp, S, (int)qb, (int)N, (int)Pq, (int)Pk, (int)pd, div};
+  p.sc = ScoreParams2{qp, kp, S, (int)qb, (int)N, (int)Pq, (int)Pk, (int)pd, div, (int)pd, 4};
   p.ids = ids;
   p.C = (int)C;
   p.out = out;

@@ -48,17 +48,22 @@ class FlatGate(nn.Module):
         return torch.stack([one(feat[l], W[l]) for l in range(feat.shape[0])])
 
     @torch.no_grad()
-    def project_key_levels(self, level_features):
+    def project_key_levels(self, level_features, interleaved=False):
         """Projects the levels of a key tree (each ``[L,G,n_v,P,d]``) into one
         table ``[L,G,sum n_v,P,p]`` with node IDs leaf-first: the values of
-        ``project_keys(torch.cat(level_features, dim=2))`` without the copy."""
+        ``project_keys(torch.cat(level_features, dim=2))`` without the copy.
+        ``interleaved=True``: the same values as ``[L,G,N,p/4,P,4]`` (the
+        traversal's fast key layout)."""
         first = level_features[0]
         L, G, _, P, d = first.shape
         if first.dtype not in (torch.bfloat16, torch.float16, torch.float32) or d % 4 or self.proj_dim % 4:
-            return self.project_keys(torch.cat(level_features, dim=2))
+            out = self.project_keys(torch.cat(level_features, dim=2))
+            if interleaved:
+                out = out.reshape(out.shape[:4] + (self.proj_dim // 4, 4)).transpose(3, 4).contiguous()
+            return out
         outs = []
         for l in range(L):
-            outs.append(project_levels([f[l] for f in level_features], self.Wk[l]))
+            outs.append(project_levels([f[l] for f in level_features], self.Wk[l], interleaved=interleaved))
         out = outs[0].unsqueeze(0) if L == 1 else torch.stack(outs)
         return out
 

@@ -84,12 +84,15 @@ def project(x, W):
     return out.reshape(x.shape[:-1] + (P,))
 
 
-def project_levels(levels, W):
+def project_levels(levels, W, interleaved=False):
     """Projection of prototype rows kept in several buffers: ``levels`` is a
     list of ``[S, n_v, P, D]`` tensors (bf16, f16 or float32, one dtype; the
     levels of a key tree, leaf first) and the result is ``[S, sum n_v, P, p]``
     float32, level after level along the node axis.  The same values as
-    ``project(torch.cat(levels, dim=1).float(), W)``, without the copies."""
+    ``project(torch.cat(levels, dim=1).float(), W)``, without the copies.
+    ``interleaved=True`` returns the same values as ``[S, N, p/4, P, 4]``
+    (each node's prototypes interleaved by 4-float group), the key layout
+    the tree traversal reads fastest."""
     if not levels:
         raise ValueError("levels must not be empty")
     for t in levels:
@@ -104,13 +107,17 @@ def project_levels(levels, W):
     W = W.to(device=levels[0].device, dtype=torch.float32).contiguous()
     bufs = [t.contiguous() for t in levels]
     nodes = [t.shape[1] for t in bufs]
-    out = torch.empty((S, sum(nodes), P, W.shape[1]), device=bufs[0].device, dtype=torch.float32)
+    p = W.shape[1]
+    if interleaved and p % 4:
+        raise ValueError("the interleaved layout needs a projection dim divisible by 4")
+    shape = (S, sum(nodes), p // 4, P, 4) if interleaved else (S, sum(nodes), P, p)
+    out = torch.empty(shape, device=bufs[0].device, dtype=torch.float32)
     ptrs = (ctypes.c_void_p * len(bufs))(*[t.data_ptr() for t in bufs])
     counts = (ctypes.c_int64 * len(bufs))(*nodes)
     with torch.cuda.device(bufs[0].device):
         rc = spruce_hip.lib().spruce_gate_project_levels(
             ptrs, counts, len(bufs), S, P, D, spruce_hip.dtype_code(bufs[0]), spruce_hip.ptr(W), W.shape[1],
-            spruce_hip.ptr(out), spruce_hip.stream_of(bufs[0]))
+            spruce_hip.ptr(out), 1 if interleaved else 0, spruce_hip.stream_of(bufs[0]))
     spruce_hip.check(rc, "spruce_gate_project_levels")
     return out
 

@@ -47,13 +47,27 @@ def output_width(num_leaves, radix, beam):
     return width
 
 
-def traverse_projected(projected_q, projected_k_all, num_leaves, beam, radix, div):
+def traverse_projected(projected_q, projected_k_all, num_leaves, beam, radix, div, rows_kernel=False):
     """Raw form: projected_q [L,G,qb,Pq,p], projected_k_all [L,G,N,Pk,p]
-    (every node, leaf-first IDs) float32 -> [L,G,qb,C] int64 leaf IDs."""
+    (every node, leaf-first IDs) or the interleaved [L,G,N,p/4,Pk,4] of
+    ``FlatGate.project_key_levels(..., interleaved=True)``, float32 ->
+    [L,G,qb,C] int64 leaf IDs (the same for both layouts).  A rows-layout
+    table is copied into the interleaved layout first (the walk reads it
+    about twice as fast, which pays for the copy), unless ``rows_kernel``
+    asks for the kernel that reads the rows layout in place."""
     L, G, qb, Pq, p = projected_q.shape
-    N, Pk = projected_k_all.shape[2], projected_k_all.shape[3]
-    if projected_k_all.shape[:2] != (L, G) or projected_k_all.shape[4] != p:
+    interleaved = projected_k_all.dim() == 6
+    if interleaved:
+        N, Pk = projected_k_all.shape[2], projected_k_all.shape[4]
+        ok = projected_k_all.shape[3] * 4 == p and projected_k_all.shape[5] == 4
+    else:
+        N, Pk = projected_k_all.shape[2], projected_k_all.shape[3]
+        ok = projected_k_all.dim() == 5 and projected_k_all.shape[4] == p
+    if projected_k_all.shape[:2] != (L, G) or not ok:
         raise ValueError("projected query and key shapes disagree")
+    if not interleaved and not rows_kernel and p % 4 == 0:
+        projected_k_all = projected_k_all.reshape(L, G, N, Pk, p // 4, 4).transpose(3, 4)
+        interleaved = True
     qp = projected_q.float().contiguous()
     kp = projected_k_all.float().contiguous()
     C = output_width(num_leaves, radix, beam)
@@ -61,7 +75,7 @@ def traverse_projected(projected_q, projected_k_all, num_leaves, beam, radix, di
     with torch.cuda.device(qp.device):
         rc = spruce_hip.lib().spruce_tree_traverse(
             spruce_hip.ptr(qp), spruce_hip.ptr(kp), L * G, qb, num_leaves, Pq, Pk, p, radix, beam,
-            float(div), spruce_hip.ptr(out), C, spruce_hip.stream_of(qp))
+            float(div), spruce_hip.ptr(out), C, 1 if interleaved else 0, spruce_hip.stream_of(qp))
     spruce_hip.check(rc, "spruce_tree_traverse")
     return out.long()
 
@@ -86,7 +100,7 @@ def traverse_to_leaf_ids(gate, q_feat, key_levels, beam, radix=2, layer_chunk=1)
         raise RuntimeError("traverse_to_leaf_ids (HIP) requires GPU tensors")
     projected_q = gate.project_queries(q_feat)
     if hasattr(gate, "project_key_levels"):
-        projected_k = gate.project_key_levels([lvl.features for lvl in key_levels])
+        projected_k = gate.project_key_levels([lvl.features for lvl in key_levels], interleaved=True)
     else:
         projected_k = gate.project_keys(torch.cat([lvl.features for lvl in key_levels], dim=2))
     return traverse_projected(projected_q, projected_k, kb, beam, radix, math.sqrt(gate.proj_dim))

@@ -52,7 +52,7 @@ _SIGNATURES = {
     "spruce_gate_project": [_p, _p, _i64, _i64, _i64, _p, _p],
     "spruce_gate_project2": [_p, _p, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _p],
     "spruce_gate_project_levels": [ctypes.POINTER(_p), _STRIDES, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _i64,
-                                   _p, _p],
+                                   _p, ctypes.c_int, _p],
     "spruce_gate_scores": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int, _p, _p],
     "spruce_causal_topk": [_p, _i64, _i64, _i64, _i64, _p, _p],
     "spruce_teacher_block_mass": [
@@ -92,7 +92,8 @@ _SIGNATURES = {
     "spruce_residual_frontier": [_p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p],
     "spruce_tree_merge_level": [_p, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _p],
     "spruce_tree_merge_levels": [_p, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _i64, _p],
-    "spruce_tree_traverse": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _p, _i64, _p],
+    "spruce_tree_traverse": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _p, _i64,
+                             ctypes.c_int, _p],
     "spruce_gate_candidate_scores": [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, _p, _p],
     "spruce_sparse_prefill_mask": [
         _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _i64,

@@ -101,8 +101,10 @@ def test_tree_merge_levels_validation_before_launch():
     assert "radix * P must be <= 64" in spruce_hip.last_error()
     # Traversal: beam * radix is bounded the same way.
     for beam, radix in ((1 << 62, 4), (4, 1 << 62), (33, 2)):
-        assert lib.spruce_tree_traverse(fake, fake, 1, 4, 8, 1, 1, 16, radix, beam, 1.0, fake, 4, None) == -1
+        assert lib.spruce_tree_traverse(fake, fake, 1, 4, 8, 1, 1, 16, radix, beam, 1.0, fake, 4, 0, None) == -1
         assert "beam * radix must be <= 64" in spruce_hip.last_error()
+    assert lib.spruce_tree_traverse(fake, fake, 1, 4, 8, 1, 1, 16, 2, 4, 1.0, fake, 4, 2, None) == -1
+    assert "unknown key table layout" in spruce_hip.last_error()
 
 
 def test_error_codes_map_to_reference_exception_types():
@@ -145,13 +147,14 @@ def test_project_levels_validation_before_launch():
     fake = ctypes.c_void_p(1 << 20)
     levels = (ctypes.c_void_p * 2)(fake, fake)
     nodes = (ctypes.c_int64 * 2)(4, 2)
-    cases = [((levels, nodes, 0, 1, 8, 128, 0, fake, 128, fake, None), "between 1 and 32 levels"),
-             ((levels, nodes, 33, 1, 8, 128, 0, fake, 128, fake, None), "between 1 and 32 levels"),
-             ((levels, nodes, 2, 1, 8, 126, 0, fake, 128, fake, None), "multiples of 4"),
-             ((levels, nodes, 2, 1, 8, 128, 9, fake, 128, fake, None), "unsupported dtype"),
-             (((ctypes.c_void_p * 2)(fake, None), nodes, 2, 1, 8, 128, 0, fake, 128, fake, None), "level 1"),
+    cases = [((levels, nodes, 0, 1, 8, 128, 0, fake, 128, fake, 0, None), "between 1 and 32 levels"),
+             ((levels, nodes, 33, 1, 8, 128, 0, fake, 128, fake, 0, None), "between 1 and 32 levels"),
+             ((levels, nodes, 2, 1, 8, 126, 0, fake, 128, fake, 0, None), "multiples of 4"),
+             ((levels, nodes, 2, 1, 8, 128, 9, fake, 128, fake, 0, None), "unsupported dtype"),
+             (((ctypes.c_void_p * 2)(fake, None), nodes, 2, 1, 8, 128, 0, fake, 128, fake, 0, None), "level 1"),
              (((ctypes.c_void_p * 2)(fake, ctypes.c_void_p((1 << 20) + 2)), nodes, 2, 1, 8, 128, 0, fake, 128,
-               fake, None), "not 8-byte aligned")]
+               fake, 0, None), "not 8-byte aligned"),
+             ((levels, nodes, 2, 1, 8, 128, 0, fake, 128, fake, 3, None), "unknown output layout")]
     for args, message in cases:
         assert lib.spruce_gate_project_levels(*args) == -1, message
         assert message in spruce_hip.last_error(), (message, spruce_hip.last_error())

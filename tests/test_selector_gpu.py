@@ -121,6 +121,10 @@ def test_projection_of_levels_equals_projection_of_their_float_copy(dtype, S, no
     flat = torch.cat(levels, dim=1).float()
     assert got.shape == (S, sum(nodes), Pk, P)
     assert torch.equal(got, project(flat.to(DEV), W))
+    # The interleaved layout holds the same values: [S, N, P/4, Pk, 4].
+    il = project_levels([t.to(DEV) for t in levels], W.to(DEV), interleaved=True)
+    assert il.shape == (S, sum(nodes), P // 4, Pk, 4)
+    assert torch.equal(il, got.reshape(S, sum(nodes), Pk, P // 4, 4).transpose(2, 3))
     if flat.numel() * P <= 1 << 24:
         assert np.array_equal(_np(got).reshape(-1, P), osel.project(flat.reshape(-1, D).numpy(), W.numpy()))
 
@@ -131,7 +135,12 @@ def test_flat_gate_key_levels_and_model_dtype_queries():
     q = torch.randn(2, 3, 40, 4, 64, generator=gen).to(torch.bfloat16).to(DEV)
     levels = [torch.randn(2, 3, n, 4, 64, generator=gen).to(torch.bfloat16).to(DEV) for n in (40, 20, 10, 5, 3, 2, 1)]
     with torch.no_grad():
-        assert torch.equal(gate.project_key_levels(levels), gate.project_keys(torch.cat(levels, dim=2).float()))
+        rows = gate.project_keys(torch.cat(levels, dim=2).float())
+        assert torch.equal(gate.project_key_levels(levels), rows)
+        il = rows.reshape(2, 3, 81, 4, 8, 4).transpose(3, 4)
+        assert torch.equal(gate.project_key_levels(levels, interleaved=True), il)
+        # Features the kernel does not read directly (float64) take project_keys, then the same layout.
+        assert torch.equal(gate.project_key_levels([x.double() for x in levels], interleaved=True), il)
         assert torch.equal(gate.project_queries(q), gate.project_queries(q.float()))
 
 
