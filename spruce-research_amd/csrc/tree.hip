@@ -58,6 +58,15 @@ __device__ __forceinline__ void store_elem(void* base, int64_t i, float v, int d
   }
 }
 
+// Order-preserving 32-bit image of a score: larger score -> larger image,
+// every NaN the largest, -0 and +0 equal (the order of ranks_before).
+__device__ __forceinline__ uint32_t score_order(float x) {
+  if (x != x) return 0xffffffffu;
+  if (x == 0.f) return 0x80000000u;
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
 // a ranks before b: larger value first, NaN largest, ties to the lower index.
 __device__ __forceinline__ bool ranks_before(float a, int ia, float b, int ib) {
   const bool na = a != a, nb = b != b;
@@ -432,30 +441,27 @@ __global__ __launch_bounds__(64) void tree_traverse_kernel(const TraverseParams 
       }
     }
     __syncthreads();
+    // Each candidate's place in the order (valid first; then score
+    // descending, NaN first, equal scores to the lower node; invalid ones by
+    // lane) as one distinct 64-bit key, larger = earlier, so a rank is a
+    // count of larger keys: one 64-bit compare per other candidate.
+    uint64_t key = 0;
     if (lane < ncand) {
       float best = pm[lane * sc.Pk];
       for (int c = 1; c < sc.Pk; ++c)
         if (pm[lane * sc.Pk + c] > best) best = pm[lane * sc.Pk + c];
-      score[lane] = best / sc.div;
+      key = valid[lane] ? (1ull << 63) | ((uint64_t)score_order(best / sc.div) << 31) |
+                              (uint64_t)(0x7fffffff - cand[lane])
+                        : (uint64_t)(63 - lane);
     }
-    __syncthreads();
     int k = p.beam < ncand ? p.beam : ncand;
     k = k < p.count[v] ? k : p.count[v];
-    int rank = 64;
-    if (lane < ncand) {
-      const bool mine_ok = valid[lane] != 0;
-      rank = 0;
-      for (int o = 0; o < ncand; ++o) {
-        if (o == lane) continue;
-        const bool ook = valid[o] != 0;
-        bool before;
-        if (ook != mine_ok) before = ook;                 // valid candidates rank first
-        else if (!ook) before = o < lane;                  // invalid: any fixed order
-        else before = ranks_before(score[o], cand[o], score[lane], cand[lane]);
-        rank += before ? 1 : 0;
-      }
+    int rank = 0;
+    for (int o = 0; o < ncand; ++o) {
+      const uint64_t ko = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(key >> 32), o) << 32) |
+                          (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)key, o);
+      rank += ko > key ? 1 : 0;
     }
-    __syncthreads();
     if (lane < ncand && rank < k) sel[rank] = valid[lane] ? cand[lane] : -1;
     W = k;
     __syncthreads();
