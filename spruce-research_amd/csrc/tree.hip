@@ -404,8 +404,7 @@ __global__ __launch_bounds__(64) void tree_traverse_kernel(const TraverseParams 
   const int lane = threadIdx.x;
   float* qrow = sh;                          // [Pq, p]
   float* pm = qrow + sc.Pq * sc.pd;          // [64, Pk] per-(candidate, key prototype) max
-  float* score = pm + 64 * sc.Pk;            // [64]
-  int* cand = reinterpret_cast<int*>(score + 64);   // [64]
+  int* cand = reinterpret_cast<int*>(pm + 64 * sc.Pk);   // [64]
   int* valid = cand + 64;                    // [64]
   int* sel = valid + 64;                     // [64] current beam (node index within level)
   const float* qsrc = sc.qp + (s * sc.qb + q) * (int64_t)sc.Pq * sc.pd;
@@ -655,7 +654,7 @@ extern "C" int spruce_tree_traverse(const float* qp, const float* kp, int64_t S,
   p.levels = levels;
   p.C = (int)C;
   p.out = out;
-  const size_t lds = ((size_t)Pq * pd + 64 * Pk + 64) * sizeof(float) + 3 * 64 * sizeof(int);
+  const size_t lds = ((size_t)Pq * pd + 64 * Pk) * sizeof(float) + 3 * 64 * sizeof(int);
   const dim3 grid((unsigned)(S * qb));
   switch (Pq) {
     case 1: hipLaunchKernelGGL(tree_traverse_kernel<1>, grid, dim3(64), lds, (hipStream_t)stream, p); break;
