@@ -488,40 +488,50 @@ constexpr int kSchedDsRead = 0x100;
 constexpr int kLookahead = 2;
 
 // Four mask values of one row at element el (keys el .. el + 3, of which the
-// first nvalid exist), as float: bool masks give 0 (attend) or -inf.
-__device__ __forceinline__ void amask_load4(const AttnParams& p, int64_t el, int nvalid, float (&v)[4]) {
+// first nvalid exist) as raw bits, converted only when the scores need them
+// (amask_unpack4), so the loads can be issued a block ahead: f32 in w[0..3],
+// 16-bit in w[0..1] (element t in half t%2 of w[t/2]), bytes in w[0].
+// Missing elements read as zero bits.
+__device__ __forceinline__ uint4 amask_fetch4(const AttnParams& p, int64_t el, int nvalid) {
   const int dt = p.amask_dtype;
   if (p.amask_vec && nvalid >= 4) {
-    if (dt == SPRUCE_DTYPE_F32) {
-      const float4 x = *reinterpret_cast<const float4*>(static_cast<const float*>(p.amask) + el);
-      v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
-    } else if (dt == SPRUCE_DTYPE_U8) {
-      const uint32_t x = *reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.amask) + el);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) v[t] = ((x >> (8 * t)) & 0xffu) ? 0.f : -INFINITY;
-    } else {
-      const uint2 x = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.amask) + el);
-      const bool f16 = dt == SPRUCE_DTYPE_F16;
-      v[0] = f16 ? unpack1<true>(x.x & 0xffffu) : unpack1<false>(x.x & 0xffffu);
-      v[1] = f16 ? unpack1<true>(x.x >> 16) : unpack1<false>(x.x >> 16);
-      v[2] = f16 ? unpack1<true>(x.y & 0xffffu) : unpack1<false>(x.y & 0xffffu);
-      v[3] = f16 ? unpack1<true>(x.y >> 16) : unpack1<false>(x.y >> 16);
+    if (dt == SPRUCE_DTYPE_F32) return *reinterpret_cast<const uint4*>(static_cast<const float*>(p.amask) + el);
+    if (dt == SPRUCE_DTYPE_U8) {
+      return uint4{*reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(p.amask) + el), 0u, 0u, 0u};
     }
-    return;
+    const uint2 x = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.amask) + el);
+    return uint4{x.x, x.y, 0u, 0u};
   }
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    v[t] = 0.f;
     if (t < nvalid) {
       if (dt == SPRUCE_DTYPE_F32) {
-        v[t] = static_cast<const float*>(p.amask)[el + t];
+        w[t] = static_cast<const uint32_t*>(p.amask)[el + t];
       } else if (dt == SPRUCE_DTYPE_U8) {
-        v[t] = static_cast<const uint8_t*>(p.amask)[el + t] ? 0.f : -INFINITY;
+        w[0] |= (uint32_t)static_cast<const uint8_t*>(p.amask)[el + t] << (8 * t);
       } else {
-        const uint32_t x = static_cast<const uint16_t*>(p.amask)[el + t];
-        v[t] = dt == SPRUCE_DTYPE_F16 ? unpack1<true>(x) : unpack1<false>(x);
+        w[t >> 1] |= (uint32_t)static_cast<const uint16_t*>(p.amask)[el + t] << (16 * (t & 1));
       }
     }
+  }
+  return uint4{w[0], w[1], w[2], w[3]};
+}
+
+// The four values of amask_fetch4 as float: bool masks give 0 (attend) or -inf.
+__device__ __forceinline__ void amask_unpack4(int dt, const uint4& x, float (&v)[4]) {
+  if (dt == SPRUCE_DTYPE_F32) {
+    v[0] = __builtin_bit_cast(float, x.x); v[1] = __builtin_bit_cast(float, x.y);
+    v[2] = __builtin_bit_cast(float, x.z); v[3] = __builtin_bit_cast(float, x.w);
+  } else if (dt == SPRUCE_DTYPE_U8) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) v[t] = ((x.x >> (8 * t)) & 0xffu) ? 0.f : -INFINITY;
+  } else {
+    const bool f16 = dt == SPRUCE_DTYPE_F16;
+    v[0] = f16 ? unpack1<true>(x.x & 0xffffu) : unpack1<false>(x.x & 0xffffu);
+    v[1] = f16 ? unpack1<true>(x.x >> 16) : unpack1<false>(x.x >> 16);
+    v[2] = f16 ? unpack1<true>(x.y & 0xffffu) : unpack1<false>(x.y & 0xffffu);
+    v[3] = f16 ? unpack1<true>(x.y >> 16) : unpack1<false>(x.y >> 16);
   }
 }
 
@@ -787,13 +797,17 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
   // General attention mask: the 32 values this lane adds to its scores of a
   // key block (register r of key tile c holds key 32c + 8(r/4) + 4(lane/32)
   // + r%4 of query q0 + l32), loaded before the block's S^T MFMAs.
-  float am0[AMASK ? 16 : 1], am1[AMASK ? 16 : 1];
-  auto load_amask = [&](int blk) {
+  // The raw mask bits of the next block are fetched while the current one
+  // finishes (after its softmax), so their latency hides behind its P.V,
+  // the barrier and the next block's S^T MFMAs.  Group 4c + j holds keys
+  // 32c + 8j + 4(lane/32) .. + 3 of query q0 + l32.
+  uint4 amr[AMASK ? 8 : 1];
+  auto fetch_amask = [&](int blk) {
     if constexpr (AMASK) {
       const int qt = q0 + l32;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) am0[r] = am1[r] = 0.f;
-      if (qt < p.T) {
+      for (int g8 = 0; g8 < 8; ++g8) amr[g8] = uint4{0u, 0u, 0u, 0u};
+      if (qt < p.T && blk >= 0) {
         const int mh = p.amask_heads > 1 ? head : 0;
         const int64_t row = (int64_t)b * p.ams[0] + (int64_t)mh * p.ams[1] + (int64_t)qt * p.ams[2];
 #pragma unroll
@@ -801,10 +815,7 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int key0 = blk * kBlock + 32 * c + 8 * j + 4 * hl;
-            float v[4];
-            amask_load4(p, row + key0, p.T - key0, v);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) (c == 0 ? am0 : am1)[4 * j + t] = v[t];
+            amr[4 * c + j] = amask_fetch4(p, row + key0, p.T - key0);
           }
       }
     }
@@ -816,9 +827,15 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     if constexpr (AMASK) {
       // Added in raw score units: (s + mask * log2(e) / cs) * cs.
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s0[r] += am0[r] * p.amask_mul;
-        s1[r] += am1[r] * p.amask_mul;
+      for (int j = 0; j < 4; ++j) {
+        float v0[4], v1[4];
+        amask_unpack4(p.amask_dtype, amr[j], v0);
+        amask_unpack4(p.amask_dtype, amr[4 + j], v1);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          s0[4 * j + t] += v0[t] * p.amask_mul;
+          s1[4 * j + t] += v1[t] * p.amask_mul;
+        }
       }
     }
     if constexpr (KVAL) {
@@ -917,11 +934,13 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
       acc[dt] = mfma32x32x16<F16>(va[i], pk[c][h2], acc[dt]);
     }
   };
-  auto compute = [&](int buf, bool diag, const float* sb, uint64_t vb, int blk) {
+  // next_blk: the block after this one (-1: none), whose mask bits are
+  // fetched once this block's scores hold its own (AMASK only).
+  auto compute = [&](int buf, bool diag, const float* sb, uint64_t vb, int next_blk) {
     const uint16_t* Ks = smem + buf * BUF;
-    load_amask(blk);
     scores(Ks);
     softmax(diag, sb, vb);
+    fetch_amask(next_blk);
     pv(Ks + KTILE);
   };
   // Key padding: this lane's validity byte of block `blk` (loaded one block
@@ -959,13 +978,14 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
       } else {
         if (!q_ready) convert_q();
         uint32_t vcur = vbyte(cur_id);
+        fetch_amask(cur_id);
         __syncthreads();
         while (true) {
           int nid = 0;
           bool nen = false;
           const bool more = it.next(nid, nen);
           const uint32_t vnext = more ? vbyte(nid) : 0u;
-          if (active && cur_en) compute(buf, cur_id == qb, nullptr, vbits(vcur), cur_id);
+          if (active && cur_en) compute(buf, cur_id == qb, nullptr, vbits(vcur), more ? nid : -1);
           if (!more) break;
           __syncthreads();
           buf ^= 1;
@@ -977,6 +997,7 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     } else {
       uint32_t vcur = vbyte(cur_id);
       load_block(cur_id);
+      fetch_amask(cur_id);
       if (!q_ready) convert_q();
       store_block(0);
       __syncthreads();
@@ -986,7 +1007,7 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
         const bool more = it.next(nid, nen);
         const uint32_t vnext = more ? vbyte(nid) : 0u;
         if (more) load_block(nid);
-        if (active && cur_en) compute(buf, cur_id == qb, nullptr, vbits(vcur), cur_id);
+        if (active && cur_en) compute(buf, cur_id == qb, nullptr, vbits(vcur), more ? nid : -1);
         if (!more) break;
         store_block(buf ^ 1);
         __syncthreads();
