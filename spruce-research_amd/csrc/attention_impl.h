@@ -81,10 +81,12 @@ struct AttnParams {
   // (the last one 1), Hm = 1 or Hq; dtype bf16 / f16 / f32 (added to the
   // scaled score) or u8 (bool: nonzero attends, zero gives no weight).
   // amask_mul = log2(e) / cs turns a mask value into raw score units;
-  // amask_vec: 4-element groups may be read as one aligned load.
+  // amask_vec: 4-element groups may be read as one aligned load;
+  // amask_rows16: 16-byte row pieces may be read (base and row strides
+  // 16-byte aligned); amask_tk: the mask's key extent.
   const void* amask;
   int64_t ams[4];
-  int amask_dtype, amask_heads, amask_vec;
+  int amask_dtype, amask_heads, amask_vec, amask_rows16, amask_tk;
   float amask_mul;
   // residual summaries (sparse/attention.py:226-265): per row, nodes
   // [B, Hkv, Qb, S] int32 (-1 = none); table keys/values float32
@@ -799,17 +801,47 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
   // + r%4 of query q0 + l32), loaded before the block's S^T MFMAs.
   // The raw mask bits of the next block are fetched while the current one
   // finishes (after its softmax), so their latency hides behind its P.V,
-  // the barrier and the next block's S^T MFMAs.  Group 4c + j holds keys
-  // 32c + 8j + 4(lane/32) .. + 3 of query q0 + l32.
+  // the barrier and the next block's S^T MFMAs.
+  //  * Row pieces (amask_rows16, and the block's 64 keys inside the mask):
+  //    the wave's 32 query rows are read as 16-byte pieces along each row
+  //    (64 * eb bytes per row, so 2, 4 or 8 loads for 1, 2 or 4-byte
+  //    elements, each touching 64 * 16 / (64 * eb) rows' lines), then
+  //    turned into the score layout through a wave-private LDS region.
+  //    Reading each lane's 4-key groups directly instead touches 32 rows'
+  //    lines per load, 8 loads per block, and the address units bound it.
+  //  * Otherwise group 4c + j of amr holds keys 32c + 8j + 4(lane/32) .. + 3
+  //    of query q0 + l32, read directly.
   uint4 amr[AMASK ? 8 : 1];
+  bool am_rows = false;  // wave-uniform: amr holds row pieces
+  constexpr int kAmRowWords = 68;  // LDS row of the staging region: 256 + 16 bytes
+  __shared__ __attribute__((aligned(16))) uint32_t amlds[AMASK ? WAVES * 32 * kAmRowWords : 1];
   auto fetch_amask = [&](int blk) {
     if constexpr (AMASK) {
-      const int qt = q0 + l32;
 #pragma unroll
       for (int g8 = 0; g8 < 8; ++g8) amr[g8] = uint4{0u, 0u, 0u, 0u};
-      if (qt < p.T && blk >= 0) {
-        const int mh = p.amask_heads > 1 ? head : 0;
-        const int64_t row = (int64_t)b * p.ams[0] + (int64_t)mh * p.ams[1] + (int64_t)qt * p.ams[2];
+      am_rows = false;
+      if (blk < 0) return;
+      const int mh = p.amask_heads > 1 ? head : 0;
+      const int64_t rbase = (int64_t)b * p.ams[0] + (int64_t)mh * p.ams[1];
+      const int eb = p.amask_dtype == SPRUCE_DTYPE_F32 ? 4 : (p.amask_dtype == SPRUCE_DTYPE_U8 ? 1 : 2);
+      if (p.amask_rows16 && blk * kBlock + kBlock <= p.amask_tk) {
+        am_rows = true;
+        const int lpr = 4 * eb;          // lanes per row (16 bytes each)
+        const int rpi = 64 / lpr;        // rows per load
+        const int rr = lane / lpr, cb = (lane % lpr) * 16;
+        const char* mbase = static_cast<const char*>(p.amask);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int r = i * rpi + rr;
+          if (i < 32 / rpi && q0 + r < p.T)
+            amr[i] = *reinterpret_cast<const uint4*>(
+                mbase + (rbase + (int64_t)(q0 + r) * p.ams[2] + (int64_t)blk * kBlock) * eb + cb);
+        }
+        return;
+      }
+      const int qt = q0 + l32;
+      if (qt < p.T) {
+        const int64_t row = rbase + (int64_t)qt * p.ams[2];
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
@@ -820,11 +852,49 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
       }
     }
   };
+  // Row pieces -> this lane's 4-key groups, through the wave's LDS rows.
+  auto stage_amask = [&]() {
+    if constexpr (AMASK) {
+      if (!am_rows) return;
+      const int eb = p.amask_dtype == SPRUCE_DTYPE_F32 ? 4 : (p.amask_dtype == SPRUCE_DTYPE_U8 ? 1 : 2);
+      const int lpr = 4 * eb, rpi = 64 / lpr;
+      const int rr = lane / lpr, cb = (lane % lpr) * 16;
+      char* reg = reinterpret_cast<char*>(amlds + wave * 32 * kAmRowWords);
+      constexpr int RB = kAmRowWords * 4;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (i < 32 / rpi) *reinterpret_cast<uint4*>(reg + (i * rpi + rr) * RB + cb) = amr[i];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const char* mine = reg + l32 * RB + 4 * hl * eb;
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const char* src = mine + (32 * c + 8 * j) * eb;
+          if (eb == 4) {
+            amr[4 * c + j] = *reinterpret_cast<const uint4*>(src);
+          } else if (eb == 2) {
+            const uint2 x = *reinterpret_cast<const uint2*>(src);
+            amr[4 * c + j] = uint4{x.x, x.y, 0u, 0u};
+          } else {
+            amr[4 * c + j] = uint4{*reinterpret_cast<const uint32_t*>(src), 0u, 0u, 0u};
+          }
+        }
+      // The next block's stores into these rows come after these reads in
+      // the wave's own order.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+  };
   // sb: per-key score bias of a summary chunk (null for a key block).
   // vb: validity bits of the block's 64 keys (key padding; all set otherwise).
   auto softmax = [&](bool diag, const float* sb, uint64_t vb) {
     f32x16_t s0 = sc0, s1 = sc1;
     if constexpr (AMASK) {
+      stage_amask();
       // Added in raw score units: (s + mask * log2(e) / cs) * cs.
 #pragma unroll
       for (int j = 0; j < 4; ++j) {

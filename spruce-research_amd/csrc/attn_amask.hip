@@ -25,6 +25,7 @@ extern "C" int spruce_sparse_prefill_index_amask(
                  (long long)Tq, (long long)Tk, (long long)T);
   SPRUCE_REQUIRE(ams[3] == 1, "the attention mask must have a contiguous last dimension");
   SPRUCE_REQUIRE(ams[0] >= 0 && ams[1] >= 0 && ams[2] >= 0, "negative attention mask strides");
+  SPRUCE_REQUIRE(Tk < ((int64_t)1 << 30), "attention mask too wide");
   SPRUCE_REQUIRE(amask_dtype == SPRUCE_DTYPE_BF16 || amask_dtype == SPRUCE_DTYPE_F16 ||
                      amask_dtype == SPRUCE_DTYPE_F32 || amask_dtype == SPRUCE_DTYPE_U8,
                  "unsupported attention mask dtype code %d", amask_dtype);
@@ -43,6 +44,11 @@ extern "C" int spruce_sparse_prefill_index_amask(
   // multiples of 4 elements.
   p.amask_vec = ((uintptr_t)amask % (uintptr_t)(4 * eb)) == 0 && ams[0] % 4 == 0 && (Hm == 1 || ams[1] % 4 == 0) &&
                 ams[2] % 4 == 0;
+  // Whole 16-byte row pieces: the base and every row start 16-byte aligned
+  // (a block's 64 keys start at a multiple of 64 elements).
+  p.amask_rows16 = ((uintptr_t)amask % 16) == 0 && (ams[0] * eb) % 16 == 0 && (Hm == 1 || (ams[1] * eb) % 16 == 0) &&
+                   (ams[2] * eb) % 16 == 0;
+  p.amask_tk = (int)Tk;
   p.amask_mul = 1.4426950408889634f / p.cs;
   return launch_attention<kModePadded, false, false, true>(p, (int)D, dtype, shape.waves, (hipStream_t)stream);
 }

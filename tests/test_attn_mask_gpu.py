@@ -6,7 +6,9 @@ Cases: random additive masks with -inf entries (broadcast and per query
 head), packed sequences with a block-diagonal boolean mask, a bf16 padding
 mask carrying a score bias, a mask wider than the sequence with
 non-multiple-of-4 row strides (element-wise loads), a batch-broadcast mask
-(stride 0), float32 inputs, and the producer-wave and 8-wave launch shapes.
+(stride 0), float32 inputs, and the producer-wave and 8-wave launch shapes;
+masks whose rows are 16-byte aligned (read as row pieces through LDS) in
+every element size, with a ragged last block read element-wise.
 
 Bar: 2e-2 max-abs / 1e-3 mean-abs against the float32 oracle
 (oracle/attention.py, add_mask) at query rows that keep at least one listed
@@ -104,7 +106,9 @@ def _oracle(q, k, v, sel, mask):
     (28, 4, 700, 128, torch.bfloat16, 1),    # Qwen2-7B heads, producer-wave form
     (28, 4, 700, 128, torch.bfloat16, 28),   # one mask per query head
     (8, 2, 333, 64, torch.float16, 8),       # G=4, full 8-wave parts
-    (6, 2, 260, 128, torch.float32, 1),
+    (6, 2, 260, 128, torch.float32, 1),      # 16-byte rows: row pieces, last block element-wise
+    (28, 4, 512, 128, torch.bfloat16, 28),   # 16-byte rows, per head, producer form
+    (8, 2, 448, 64, torch.float16, 1),       # 16-byte rows, 8-wave parts
 ])
 def test_random_additive_mask_matches_oracle(Hq, Hkv, T, D, dtype, Hm):
     seed = T + Hq + Hm
@@ -239,3 +243,18 @@ def test_zero_mask_equals_no_mask_and_residual_summaries_reject_other_masks():
             _Module(), qd, kd, vd, bias, selected_blocks=sel.to(DEV), block_size=64,
             validate_selected_blocks_input=False, residual_summaries=True,
             residual_summary_nodes=nodes.to(DEV), validate_residual_summary_nodes_input=False)
+
+
+@pytest.mark.parametrize("Hm", [1, 8])
+def test_bool_mask_in_16_byte_rows(Hm):
+    # T = 320: a bool row is 320 bytes, so blocks are read as row pieces.
+    T, Hq, Hkv, D = 320, 8, 2, 128
+    q, k, v = _qkv(61 + Hm, 2, Hq, Hkv, T, D, torch.bfloat16)
+    sel = _selection(61 + Hm, 2, Hkv, T)
+    gen = torch.Generator().manual_seed(62 + Hm)
+    mask = torch.rand(2, Hm, T, T, generator=gen) < 0.8
+    qd, kd, vd = _dev(q, k, v)
+    out = direct_index_sparse_prefill(qd, kd, vd, sel[:, 0].contiguous().to(DEV), scale=D ** -0.5,
+                                      attn_mask=mask.to(DEV))
+    torch.cuda.synchronize()
+    _check(out, _oracle(q, k, v, sel, mask), f"bool rows Hm{Hm}", _surviving(sel, mask, Hq))
