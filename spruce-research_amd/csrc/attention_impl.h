@@ -545,7 +545,7 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
   static_assert(!KVAL || MODE == kModePadded, "key padding is supported for padded block lists");
   static_assert(!AMASK || (MODE == kModePadded && !SUMM && !KVAL && !CAP),
                 "the general attention mask is supported for padded block lists without summaries");
-  static_assert(!PROD || (!SUMM && TIn::bytes == 2), "the producer form stages 16-bit K/V for key blocks only");
+  static_assert(!PROD || TIn::bytes == 2, "the producer form stages 16-bit K/V");
   constexpr int NTHR = WAVES * 64;
   constexpr int KSTR = D + 8;        // K tile row stride, 16-bit elements (16 B pad)
   constexpr int VSTR = kBlock + 8;   // V^T tile row stride
@@ -1287,7 +1287,7 @@ int launch_attention_w(const AttnParams& p, int waves, hipStream_t stream) {
     case 4: return launch_attention_t<D, 4, TIn, F16, MODE, SUMM, false, false, KVAL, AMASK>(p, stream);
     case 8:
       // A spare wave becomes the K/V producer (16-bit inputs, key blocks only).
-      if constexpr (kUseProducer && TIn::bytes == 2 && !SUMM)
+      if constexpr (kUseProducer && TIn::bytes == 2)
         if (p.tpp < 8) return launch_attention_t<D, 8, TIn, F16, MODE, SUMM, false, true, KVAL, AMASK>(p, stream);
       return launch_attention_t<D, 8, TIn, F16, MODE, SUMM, false, false, KVAL, AMASK>(p, stream);
     default: return set_error(SPRUCE_EINVAL, "unsupported wave count %d", waves);

@@ -20,6 +20,7 @@ the first violation in row order with the reference's message.
 """
 from __future__ import annotations
 
+import functools
 from dataclasses import dataclass
 from typing import Iterable, Sequence
 
@@ -72,10 +73,17 @@ class ResidualTreeLayout:
 
 
 def build_residual_tree_layout(num_leaves: int) -> ResidualTreeLayout:
-    """Node ID and leaf-range table of the tree over ``num_leaves`` key blocks."""
+    """Node ID and leaf-range table of the tree over ``num_leaves`` key blocks.
+
+    The layout depends only on the leaf count and is immutable, so each count
+    is built once (a layer's attention call asks for it every time)."""
     if num_leaves < 1:
         raise ValueError(f"num_leaves must be >= 1, got {num_leaves}")
-    n = int(num_leaves)
+    return _tree_layout(int(num_leaves))
+
+
+@functools.lru_cache(maxsize=64)
+def _tree_layout(n: int) -> ResidualTreeLayout:
     counts = [n]
     while counts[-1] > 1:
         counts.append((counts[-1] + 1) // 2)
