@@ -33,6 +33,7 @@ A boolean mask attends where True (Transformers' convention); the reference
 adds a boolean mask's 0/1 values to the scores like a float mask.
 """
 import math
+import weakref
 from typing import Optional
 
 import torch
@@ -91,6 +92,27 @@ def _validate_inputs(query, key, value, selected_blocks, block_size, layer_idx, 
         raise ValueError(
             f"selected_blocks has {query_blocks} query blocks; expected {expected_blocks} "
             f"for seq_len={query.shape[-2]} and block_size={block_size}")
+
+
+_EMPTY_ROWS = [None]   # (weakref to selected_blocks, its version, {layer: first empty row})
+
+
+def _empty_rows(selected_blocks: torch.Tensor) -> dict:
+    """{layer: (batch, kv_head, query_block) of its first row with no listed
+    block}, for every layer of ``selected_blocks`` at once.  Reading the
+    answer back waits for the GPU, so it is done once per selected_blocks
+    tensor (the model's layers share one) and kept while the tensor is alive
+    and unmodified, instead of stalling the host at every layer."""
+    last = _EMPTY_ROWS[0]
+    if last is not None and last[0]() is selected_blocks and last[1] == selected_blocks._version:
+        return last[2]
+    empty = ~(selected_blocks >= 0).any(dim=-1)        # [B, L, G, Qb]
+    found = {}
+    if bool(empty.any()):
+        for b, layer, g, qb in torch.nonzero(empty).tolist():
+            found.setdefault(layer, (b, g, qb))
+    _EMPTY_ROWS[0] = (weakref.ref(selected_blocks), selected_blocks._version, found)
+    return found
 
 
 def _check_mask_shape(attention_mask: torch.Tensor, batch: int, heads: int, seq_len: int) -> None:
@@ -208,9 +230,9 @@ def sparse_prefill_attention_forward(
         raise ValueError("the HIP sparse-prefill kernel requires block_size=64")
     indices = selected_blocks[:, layer_idx].to(device=query.device, dtype=torch.int32).contiguous()
     # The reference raises on a row with no selected block (sparse/attention.py:192-199).
-    empty = ~(indices >= 0).any(dim=-1)
-    if bool(empty.any()):
-        b, g, qb = (int(x) for x in torch.nonzero(empty)[0])
+    empty_row = _empty_rows(selected_blocks).get(layer_idx)
+    if empty_row is not None:
+        b, g, qb = empty_row
         raise ValueError(
             "selected_blocks leaves an attention row empty at "
             f"batch={b}, layer={layer_idx}, kv_head={g}, query_block={qb}")

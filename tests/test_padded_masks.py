@@ -100,3 +100,19 @@ def test_malformed_masks_raise(case):
         mask, match = mask[:1], "does not match"
     with pytest.raises(ValueError, match=match):
         _check_mask_shape(mask, 2, 4, 8)
+
+
+def test_empty_rows_are_found_per_layer_and_rechecked_after_changes():
+    from sparse.attention import _empty_rows
+    sel = torch.zeros(2, 3, 2, 4, 2, dtype=torch.int32)        # [B, L, G, Qb, K]
+    sel[1, 1, 0, 3] = -1
+    sel[0, 1, 1, 2] = -1
+    sel[1, 2, 1, 0] = -1
+    # The first empty row of each layer in (batch, kv_head, query_block) order.
+    assert _empty_rows(sel) == {1: (0, 1, 2), 2: (1, 1, 0)}
+    assert _empty_rows(sel) is _empty_rows(sel)                 # one check per tensor
+    sel[0, 0, 0, 0] = -1                                        # in place: checked again
+    assert _empty_rows(sel) == {0: (0, 0, 0), 1: (0, 1, 2), 2: (1, 1, 0)}
+    other = sel.clone()
+    other[0, 0, 0, 0] = 5
+    assert _empty_rows(other) == {1: (0, 1, 2), 2: (1, 1, 0)}
