@@ -400,6 +400,40 @@ def main():
                       "then Q prototypes pooled from the grouped tokens",
         }
 
+    # ---- residual summaries on the cfg2 selection: the frontier nodes of
+    # every row, the layer's K/V summary table (one prototype per node) and
+    # the direct-index kernel with the summary keys appended, against the
+    # same kernel without them.  FLOPs count the exact keys plus the listed
+    # summary keys.
+    if not args.no_extra:
+        from interfaces.residual_summaries import build_residual_summary_nodes, build_residual_tree_layout
+        from kernels.direct_index import direct_index_sparse_prefill, direct_index_sparse_summaries
+        from sparse.summaries import build_kv_summary_table
+        sel_r = workloads.mask_to_selected_blocks(mask[:, ::Hq // Hkv])[:, None].to(dev)
+        idx_r = sel_r[:, 0].contiguous()
+        nodes_r = build_residual_summary_nodes(sel_r, validate_selected=False)[:, 0].to(torch.int32).contiguous()
+        lay_r = build_residual_tree_layout(idx_r.shape[2])
+
+        def fnr():
+            table = build_kv_summary_table(k, v, lay_r, block_size=64, prototypes=1)
+            return direct_index_sparse_summaries(q, k, v, idx_r, nodes_r, table, scale=scale)
+
+        fnp_ = lambda: direct_index_sparse_prefill(q, k, v, idx_r, scale=scale)  # noqa: E731
+        _, krms_ = _time_launches(fnr, max(5, args.steps // 5), max(2, args.warmup // 5))
+        _, kpms_ = _time_launches(fnp_, max(5, args.steps // 5), max(2, args.warmup // 5))
+        mr_, mp_ = statistics.median(krms_), statistics.median(kpms_)
+        entries = int((nodes_r >= 0).sum())
+        flr = flops + entries * (Hq // Hkv) * BLOCK_FLOPS // 64
+        configs["cfg2_residual_summaries_32k"] = {
+            "ms_median": round(mr_, 4), "ms_min": round(min(krms_), 4), "ms_max": round(max(krms_), 4),
+            "tflops": round(flr / (mr_ * 1e-3) / 1e12, 2),
+            "frac_bf16_peak": round(flr / (mr_ * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "flop": flr, "summary_keys": entries, "prototypes": 1,
+            "without_summaries_ms_median": round(mp_, 4),
+            "stages": "K/V summary table of the layer, then direct-index attention over the listed "
+                      "blocks and the row's frontier-node summary keys in one softmax",
+        }
+
     # ---- cfg3: selector front end, T=65536 (1024 key blocks), top-32
     if not args.no_extra:
         from selector.select import select_blocks
