@@ -266,8 +266,8 @@ def main():
         "tflops": round(flops1 / (m1 * 1e-3) / 1e12, 2),
         "frac_bf16_peak": round(flops1 / (m1 * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "selected_head_blocks": sel1, "flop": flops1, "input_dtype": "fp32",
-        "note": "1 workgroup per (KV head, query block, part): 256 workgroups fill at most a quarter "
-                "of the 256 CUs' slots for a few blocks each, so this small case is launch- and "
+        "note": "128 (KV head, query block) rows split into 2 four-wave parts: 256 workgroups, "
+                "one per CU, each over a few blocks, so this small case is launch- and "
                 "latency-bound",
     }
     if not args.no_cpu:

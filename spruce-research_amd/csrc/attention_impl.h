@@ -1269,6 +1269,27 @@ inline LaunchShape choose_shape(int variant, int G) {
   return tiles % 4 == 0 ? LaunchShape{4, tiles / 4, 4} : LaunchShape{2, tiles / 2, 2};
 }
 
+// Block-sparse launches with fewer workgroups than the part has CUs (short
+// sequences, few KV heads: 128 rows of one 8-wave part at the reference's
+// T = 4096, 8/2-head case) leave CUs idle for the whole launch; there the
+// rows are split into 4- or 2-wave parts (one wave per tile) until every CU
+// has one, since a second fetch of a row's K/V blocks costs less than an
+// idle CU.  Every shape computes the same attention.
+constexpr int64_t kComputeUnits = 256;  // MI355X
+inline void split_small_grid(AttnParams& p, LaunchShape& s, int variant) {
+  if (variant == SPRUCE_VARIANT_SINGLE_HEAD_QTILE) return;
+  const int64_t rows = (int64_t)p.B * p.Hkv * p.Qb;
+  const int tiles = 2 * p.G;
+  while (rows * s.parts < kComputeUnits && s.waves > 2) {
+    if (s.waves == 8 && tiles % 4 == 0)
+      s = LaunchShape{4, tiles / 4, 4};
+    else
+      s = LaunchShape{2, tiles / 2, 2};
+  }
+  p.parts = s.parts;
+  p.tpp = s.tpp;
+}
+
 template <int D, int WAVES, typename TIn, bool F16, int MODE, bool SUMM, bool CAP = false, bool PROD = false,
           bool KVAL = false, bool AMASK = false>
 int launch_attention_t(const AttnParams& p, hipStream_t stream) {

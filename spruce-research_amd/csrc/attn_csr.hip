@@ -14,6 +14,7 @@ extern "C" int spruce_sparse_prefill_csr(
   int rc = prepare_attention(p, q, qs, k, ks, v, vs, B, Hq, Hkv, T, D, scale, dtype, variant, out, os,
                              shape);
   if (rc) return rc;
+  split_small_grid(p, shape, variant);
   SPRUCE_REQUIRE(indptr != nullptr && indices != nullptr, "indptr and indices must be non-null");
   SPRUCE_REQUIRE(nnz >= 0 && nnz < ((int64_t)1 << 31), "invalid nnz %lld", (long long)nnz);
   p.indptr = indptr;

@@ -16,6 +16,7 @@ extern "C" int spruce_sparse_prefill_index(
   int rc = prepare_attention(p, q, qs, k, ks, v, vs, B, Hq, Hkv, T, D, scale, dtype, variant, out, os,
                              shape);
   if (rc) return rc;
+  split_small_grid(p, shape, variant);
   SPRUCE_REQUIRE(idx != nullptr && is != nullptr, "indices must be a non-null device pointer");
   SPRUCE_REQUIRE(K >= 0 && K < (int64_t)1 << 30, "invalid index row width K=%lld", (long long)K);
   p.idx = idx;
@@ -66,6 +67,7 @@ extern "C" int spruce_sparse_prefill_index_summaries(
   int rc = prepare_attention(p, q, qs, k, ks, v, vs, B, Hq, Hkv, T, D, scale, dtype, variant, out, os,
                              shape);
   if (rc) return rc;
+  split_small_grid(p, shape, variant);
   SPRUCE_REQUIRE(idx != nullptr && is != nullptr, "indices must be a non-null device pointer");
   SPRUCE_REQUIRE(K >= 0 && K < (int64_t)1 << 30, "invalid index row width K=%lld", (long long)K);
   rc = set_summaries(p, nodes, ns, S, sum_keys, sum_values, sum_log_counts, N, P);
@@ -92,6 +94,7 @@ extern "C" int spruce_sparse_prefill_index_masked(
   int rc = prepare_attention(p, q, qs, k, ks, v, vs, B, Hq, Hkv, T, D, scale, dtype, variant, out, os,
                              shape);
   if (rc) return rc;
+  split_small_grid(p, shape, variant);
   SPRUCE_REQUIRE(idx != nullptr && is != nullptr, "indices must be a non-null device pointer");
   SPRUCE_REQUIRE(K >= 0 && K < (int64_t)1 << 30, "invalid index row width K=%lld", (long long)K);
   SPRUCE_REQUIRE(key_valid != nullptr, "key_valid must be a non-null device pointer");

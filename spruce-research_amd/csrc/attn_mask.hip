@@ -15,6 +15,7 @@ extern "C" int spruce_sparse_prefill_mask(
   int rc = prepare_attention(p, q, qs, k, ks, v, vs, B, Hq, Hkv, T, D, scale, dtype, variant, out, os,
                              shape);
   if (rc) return rc;
+  split_small_grid(p, shape, variant);
   SPRUCE_REQUIRE(mask != nullptr && ms != nullptr, "mask must be a non-null device pointer");
   SPRUCE_REQUIRE(Hm == Hq || Hm == Hkv, "mask heads (%lld) must equal query heads (%lld) or KV heads (%lld)",
                  (long long)Hm, (long long)Hq, (long long)Hkv);
