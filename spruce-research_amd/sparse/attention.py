@@ -102,16 +102,22 @@ def _empty_rows(selected_blocks: torch.Tensor) -> dict:
     block}, for every layer of ``selected_blocks`` at once.  Reading the
     answer back waits for the GPU, so it is done once per selected_blocks
     tensor (the model's layers share one) and kept while the tensor is alive
-    and unmodified, instead of stalling the host at every layer."""
+    and unmodified, instead of stalling the host at every layer.  Tensors
+    made under ``torch.inference_mode`` have no version counter, so an
+    in-place change to them could not be seen: they are checked at every
+    call."""
+    tracked = not selected_blocks.is_inference()
     last = _EMPTY_ROWS[0]
-    if last is not None and last[0]() is selected_blocks and last[1] == selected_blocks._version:
+    if (tracked and last is not None and last[0]() is selected_blocks
+            and last[1] == selected_blocks._version):
         return last[2]
     empty = ~(selected_blocks >= 0).any(dim=-1)        # [B, L, G, Qb]
     found = {}
     if bool(empty.any()):
         for b, layer, g, qb in torch.nonzero(empty).tolist():
             found.setdefault(layer, (b, g, qb))
-    _EMPTY_ROWS[0] = (weakref.ref(selected_blocks), selected_blocks._version, found)
+    if tracked:
+        _EMPTY_ROWS[0] = (weakref.ref(selected_blocks), selected_blocks._version, found)
     return found
 
 

@@ -222,6 +222,17 @@ def test_sparse_attention_entry_point_drop_in():
     with pytest.raises(ValueError, match="row empty"):
         sparse_prefill_attention_forward(_Module(), *dev, None, selected_blocks=bad.to(DEV),
                                          block_size=64, validate_selected_blocks_input=False)
+    # Under inference_mode (how the reference's scripts run the model) the
+    # route is an inference tensor without a version counter.
+    with torch.inference_mode():
+        sel_i = sel.to(DEV)
+        again, _ = sparse_prefill_attention_forward(_Module(), *dev, None, selected_blocks=sel_i,
+                                                    block_size=64)
+        assert torch.equal(again, actual)
+        sel_i[0, 0, 1, 2] = -1
+        with pytest.raises(ValueError, match="row empty"):
+            sparse_prefill_attention_forward(_Module(), *dev, None, selected_blocks=sel_i,
+                                             block_size=64, validate_selected_blocks_input=False)
 
 
 def test_full_size_cfg2_every_row_and_layout_identity():

@@ -116,3 +116,15 @@ def test_empty_rows_are_found_per_layer_and_rechecked_after_changes():
     other = sel.clone()
     other[0, 0, 0, 0] = 5
     assert _empty_rows(other) == {1: (0, 1, 2), 2: (1, 1, 0)}
+
+
+def test_empty_rows_of_inference_tensors_are_checked_at_every_call():
+    # Tensors made under inference_mode (how the reference's scripts run the
+    # model) have no version counter: no caching, in-place changes are seen.
+    from sparse.attention import _empty_rows
+    with torch.inference_mode():
+        sel = torch.zeros(1, 2, 1, 3, 2, dtype=torch.int32)
+        assert _empty_rows(sel) == {}
+        sel[0, 1, 0, 2] = -1
+        assert _empty_rows(sel) == {1: (0, 0, 2)}
+    assert _empty_rows(sel) == {1: (0, 0, 2)}
