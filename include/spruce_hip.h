@@ -218,8 +218,9 @@ int spruce_sparse_prefill_index_masked(
  *          score (0 attends, -inf or finfo.min gives no weight); U8: boolean,
  *          nonzero attends, zero gives no weight.
  * A query row none of whose listed causal keys survives the mask writes
- * zeros.  Same launch shapes and arithmetic as spruce_sparse_prefill_index
- * otherwise.  No counterpart entry in the reference's kernels (its Triton
+ * zeros.  scale must be finite and nonzero (mask values are divided by it
+ * to reach the unscaled scores' units).  Same launch shapes and arithmetic
+ * as spruce_sparse_prefill_index otherwise.  No counterpart entry in the reference's kernels (its Triton
  * callback rejects attention masks, kernels/sparse_prefill.py:73-79); this is
  * the compute of its PyTorch path for masked prefill.
  */

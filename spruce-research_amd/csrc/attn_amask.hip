@@ -1,6 +1,8 @@
 // spruce_sparse_prefill_index_amask: padded direct-index block lists with a
 // general 4-D attention mask added to the scores (the masked prefill of
 // sparse/attention.py:223-229).
+#include <cmath>
+
 #include "attention_impl.h"
 
 using namespace spruce;
@@ -50,6 +52,10 @@ extern "C" int spruce_sparse_prefill_index_amask(
   p.amask_rows16 = ((uintptr_t)amask % 16) == 0 && (ams[0] * eb) % 16 == 0 && (Hm == 1 || (ams[1] * eb) % 16 == 0) &&
                    (ams[2] * eb) % 16 == 0;
   p.amask_tk = (int)Tk;
+  // Mask values are brought to the unscaled scores' units (one multiply
+  // before the scale's FMA), so the scale must be finite and nonzero.
   p.amask_mul = 1.4426950408889634f / p.cs;
+  SPRUCE_REQUIRE(std::isfinite(p.amask_mul) && std::isfinite(p.cs),
+                 "the attention mask entry needs a finite nonzero scale, got %g", (double)scale);
   return launch_attention<kModePadded, false, false, true>(p, (int)D, dtype, shape.waves, (hipStream_t)stream);
 }

@@ -165,10 +165,10 @@ def test_attention_mask_validation_before_launch():
     fake = ctypes.c_void_p(1 << 20)
     st = _strides(0, 0, 128, 1)
 
-    def call(amask=fake, ams=(0, 0, 64, 1), Hm=1, Tq=64, Tk=64, code=2):
+    def call(amask=fake, ams=(0, 0, 64, 1), Hm=1, Tq=64, Tk=64, code=2, scale=0.1):
         return lib.spruce_sparse_prefill_index_amask(
             fake, st, fake, st, fake, st, fake, _strides(0, 0, 1, 1), 1,
-            amask, _strides(*ams), Hm, Tq, Tk, code, 1, 4, 2, 64, 128, 0.1, 0, 0,
+            amask, _strides(*ams), Hm, Tq, Tk, code, 1, 4, 2, 64, 128, scale, 0, 0,
             fake, _strides(0, 128, 512, 1), None)
 
     cases = [(dict(amask=None), "non-null"),
@@ -177,7 +177,9 @@ def test_attention_mask_validation_before_launch():
              (dict(Tk=32), "must cover"),
              (dict(ams=(0, 0, 64, 2)), "contiguous last dimension"),
              (dict(ams=(-64, 0, 64, 1)), "negative"),
-             (dict(code=7), "mask dtype")]
+             (dict(code=7), "mask dtype"),
+             (dict(scale=0.0), "finite nonzero scale"),
+             (dict(scale=float("inf")), "finite nonzero scale")]
     for kwargs, message in cases:
         assert call(**kwargs) == -1, kwargs
         assert message in spruce_hip.last_error(), (kwargs, spruce_hip.last_error())
