@@ -1,0 +1,175 @@
+"""Seeded sweep of the block-sparse attention entries against the float32
+oracle: every entry (padded lists, CSR, block masks per KV head and per
+query head, key padding, general additive masks) over random shapes -- group
+sizes 1 to 16, 1 to 4 KV heads, batch 1 to 3, sequence lengths from a single
+token to about 1,200 (ragged last blocks), head_dim 64 and 128, bf16 / f16 /
+fp32 inputs, contiguous [B,H,T,D] or Qwen's [B,T,H,D] views, and the kernel
+variants.  Lists hold -1 padding, duplicates and future ids (ignored), and
+some rows are empty (they write zeros).
+
+Bar: 2e-2 max-abs / 1e-3 mean-abs against the oracle (the north-star
+tolerance), at every query position that keeps a listed causal key; float32
+inputs are rounded to bf16 for the matrix cores, so there the oracle takes
+the rounded inputs (and the float32 inputs under the max-abs bar).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle.attention as ora
+from kernels.block_mask import block_sparse_prefill
+from kernels.direct_index import (
+    KERNEL_VARIANTS,
+    direct_index_sparse_csr,
+    direct_index_sparse_prefill,
+)
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+MAX_ABS, MEAN_ABS = 2e-2, 1e-3
+ENTRIES = ["index", "csr", "mask_kv", "mask_q", "key_valid", "attn_mask"]
+DTYPES = [torch.bfloat16, torch.float16, torch.float32]
+
+
+def _cases(n=36, seed=2024):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        G = int(rng.choice([1, 2, 3, 4, 5, 6, 7, 8, 12, 16]))
+        Hkv = int(rng.integers(1, 5 if G <= 8 else 3))
+        T = int(rng.choice([1, 17, 64, 65, 127, 200, 333, 512, 640, 777, 1000, 1201]))
+        cases.append(dict(
+            entry=ENTRIES[i % len(ENTRIES)], B=int(rng.integers(1, 4)), Hq=G * Hkv, Hkv=Hkv, T=T,
+            D=int(rng.choice([64, 128])), dtype=DTYPES[int(rng.integers(0, 3))],
+            bthd=bool(rng.integers(0, 2)), variant=KERNEL_VARIANTS[int(rng.integers(0, len(KERNEL_VARIANTS)))],
+            seed=int(rng.integers(0, 1 << 30))))
+    return cases
+
+
+CASES = _cases()
+
+
+def _ids(case):
+    c = case
+    return f"{c['entry']}-B{c['B']}-{c['Hq']}x{c['Hkv']}-T{c['T']}-D{c['D']}-{str(c['dtype'])[6:]}"
+
+
+def _inputs(c, gen):
+    def one(H):
+        if c["bthd"]:
+            return torch.randn(c["B"], c["T"], H, c["D"], generator=gen).to(c["dtype"]).transpose(1, 2)
+        return torch.randn(c["B"], H, c["T"], c["D"], generator=gen).to(c["dtype"])
+    return one(c["Hq"]), one(c["Hkv"]), one(c["Hkv"])
+
+
+def _lists(rng, rows, Qb, K):
+    """Messy padded lists [rows, Qb, K]: -1, duplicates, future ids; about
+    one row in 12 empty, most rows list their diagonal."""
+    out = np.full((rows, Qb, K), -1, np.int32)
+    for r, qb in np.ndindex(rows, Qb):
+        if rng.random() < 1 / 12:
+            continue
+        n = int(rng.integers(1, K + 1))
+        row = list(rng.integers(-1, Qb + 2, size=n))
+        if rng.random() < 0.85:
+            row[0] = qb
+        rng.shuffle(row)
+        out[r, qb, :n] = row
+    return out
+
+
+def _dev(x):
+    """Device copy with the same strides (views keep their layout)."""
+    if x.dim() == 4 and not x.is_contiguous():
+        return x.transpose(1, 2).contiguous().to(DEV).transpose(1, 2)
+    return x.to(DEV)
+
+
+@pytest.mark.parametrize("c", CASES, ids=[_ids(c) for c in CASES])
+def test_sweep_matches_oracle(c):
+    print(f"sweep {_ids(c)} variant={c['variant']} bthd={c['bthd']}", flush=True)
+    gen = torch.Generator().manual_seed(c["seed"])
+    rng = np.random.default_rng(c["seed"])
+    B, Hq, Hkv, T, D = c["B"], c["Hq"], c["Hkv"], c["T"], c["D"]
+    Qb = (T + 63) // 64
+    scale = float(D) ** -0.5
+    q, k, v = _inputs(c, gen)
+    qn, kn, vn = (x.float().numpy() for x in (q, k, v))
+    qd, kd, vd = (_dev(x) for x in (q, k, v))
+    G = Hq // Hkv
+    ok = np.ones((B, T, Hq), bool)                      # (batch, query, head) compared
+    entry = c["entry"]
+    if entry in ("index", "key_valid", "attn_mask"):
+        idx = _lists(rng, B * Hkv, Qb, 5).reshape(B, Hkv, Qb, 5)
+        idx_d = torch.from_numpy(idx).to(DEV)
+        if entry == "index":
+            oracle = lambda q_, k_, v_: ora.sparse_attention_index(  # noqa: E731
+                q_, k_, v_, idx, scale=scale, empty="zero")
+            actual = direct_index_sparse_prefill(qd, kd, vd, idx_d, scale, kernel_variant=c["variant"])
+        elif entry == "key_valid":
+            lengths = rng.integers(1, T + 1, size=B)
+            pos = np.arange(T)[None]
+            valid = pos >= T - lengths[:, None] if rng.integers(0, 2) else pos < lengths[:, None]
+            # A query with no valid listed causal key: the oracle (as the
+            # reference) averages the listed keys uniformly, the kernel
+            # writes zeros; such rows are not compared.
+            for b, g, qb in np.ndindex(B, Hkv, Qb):
+                ids = np.unique(idx[b, g, qb])
+                ids = ids[(ids >= 0) & (ids <= qb)]
+                keys = (ids[:, None] * 64 + np.arange(64)[None]).reshape(-1)
+                keys = keys[(keys < T) & valid[b, np.minimum(keys, T - 1)]]
+                for t in range(qb * 64, min(qb * 64 + 64, T)):
+                    if ids.size and not (keys <= t).any():
+                        ok[b, t, g * G:(g + 1) * G] = False
+            oracle = lambda q_, k_, v_: ora.sparse_attention_index(  # noqa: E731
+                q_, k_, v_, idx, scale=scale, empty="zero", key_valid=valid)
+            actual = direct_index_sparse_prefill(qd, kd, vd, idx_d, scale,
+                                                 key_valid=torch.from_numpy(valid).to(DEV))
+        else:
+            Hm = int(rng.choice([1, Hq]))
+            mask = torch.randn(B, Hm, T, T, generator=gen) * 2
+            mask.masked_fill_(torch.rand(B, Hm, T, T, generator=gen) < 0.1, float("-inf"))
+            # Every query keeps its own key: a row listing its diagonal block
+            # has a finite score (rows without it list 64-key blocks, of which
+            # some keys survive the 10% of -inf).
+            mask[..., torch.arange(T), torch.arange(T)] = 0.0
+            mask = mask.to(c["dtype"])
+            oracle = lambda q_, k_, v_: ora.sparse_attention_index(  # noqa: E731
+                q_, k_, v_, idx, scale=scale, empty="zero", add_mask=mask.float().numpy())
+            actual = direct_index_sparse_prefill(qd, kd, vd, idx_d, scale, attn_mask=mask.to(DEV))
+    elif entry == "csr":
+        lists = _lists(rng, B * Hkv, Qb, 6).reshape(-1, 6)
+        rows = [r[r >= 0] for r in lists]
+        indptr = np.concatenate([[0], np.cumsum([len(r) for r in rows])]).astype(np.int32)
+        indices = np.concatenate(rows + [np.zeros(0, np.int32)]).astype(np.int32)
+        oracle = lambda q_, k_, v_: ora.sparse_attention_csr(  # noqa: E731
+            q_, k_, v_, indptr, indices, scale=scale, empty="zero")
+        actual = direct_index_sparse_csr(qd, kd, vd, torch.from_numpy(indptr).to(DEV),
+                                         torch.from_numpy(indices).to(DEV), scale,
+                                         kernel_variant=c["variant"])
+    else:
+        Hm = Hkv if entry == "mask_kv" else Hq
+        mask = rng.random((B, Hm, Qb, Qb)) < 0.35
+        oracle = lambda q_, k_, v_: ora.sparse_attention_mask(  # noqa: E731
+            q_, k_, v_, mask, scale=scale, empty="zero")
+        actual = block_sparse_prefill(qd, kd, vd, torch.from_numpy(mask).to(DEV), scale).transpose(1, 2)
+    torch.cuda.synchronize()
+    a = actual.float().cpu().numpy()
+    assert np.isfinite(a[ok]).all()
+
+    def err(expected):
+        assert a.shape == expected.shape == (B, T, Hq, D)
+        d = np.abs(a.astype(np.float64) - expected)[ok]
+        return (float(d.max()), float(d.mean())) if d.size else (0.0, 0.0)
+    if c["dtype"] == torch.float32:
+        # float32 inputs are rounded to bf16 for the matrix cores: the bar
+        # holds against the oracle on the rounded inputs, and the max-abs
+        # bar also against the float32 inputs (on a few short rows the
+        # rounding alone moves the mean past 1e-3).
+        mx32, mn32 = err(oracle(qn, kn, vn))
+        print(f"  float32 inputs: max_abs={mx32:.3e} mean_abs={mn32:.3e}", flush=True)
+        assert mx32 <= MAX_ABS, mx32
+        qn, kn, vn = (x.to(torch.bfloat16).float().numpy() for x in (q, k, v))
+    mx, mn = err(oracle(qn, kn, vn))
+    print(f"  max_abs={mx:.3e} mean_abs={mn:.3e}", flush=True)
+    assert mx <= MAX_ABS and mn <= MEAN_ABS, (mx, mn)
