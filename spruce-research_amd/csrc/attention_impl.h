@@ -19,9 +19,10 @@
 //     row max / row sum of the online softmax are per-lane register reductions
 //     plus one exchange with lane ^ 32;
 //   * O^T = V^T P^T takes P straight from the S^T accumulators as the B
-//     operand; V is transposed while it is staged into LDS, with its 64 keys
-//     stored in the order the accumulator layout hands them out (key bits 2
-//     and 3 swapped), so every MFMA operand is one 16-byte LDS read;
+//     operand; V is staged into LDS as it is stored (row-major, like K) and
+//     its V^T operands come from gfx950's transposing LDS reads
+//     (ds_read_b64_tr_b16, two per operand), picking the keys in the order
+//     the accumulator layout hands them out;
 //   * K/V staging is double-buffered: the next block's global loads are in
 //     flight while the current block is on the matrix cores; one barrier per
 //     block.  When a workgroup has a wave without a tile (G = 3, 5, 6, 7 in
@@ -135,10 +136,16 @@ __device__ __forceinline__ uint32_t elem16(const uint4& r, int e) {
   return (e & 1) ? (w >> 16) : (w & 0xffffu);
 }
 
-// Position of key `key` (0..63) inside a V^T row: bits 2 and 3 swapped, which
-// is the order in which the S^T accumulator registers present the keys.
-__device__ __forceinline__ int vt_pos(int key) {
-  return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
+// V^T operand from a row-major V tile ([key][d], 16-bit elements) by the
+// gfx950 transposing LDS read: within each 16-lane group, result lane i
+// element j is element i % 4 of the 4 consecutive values that source lane
+// i / 4 + 4 j points at.  Two reads give a lane the 8 keys of its MFMA
+// k-positions for one d.
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
+  const v4i16_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4i16_t*)(const_cast<uint16_t*>(p)));
+  return __builtin_bit_cast(uint2, r);
 }
 
 // ------------------------------------------------------------ block lists
@@ -354,20 +361,6 @@ __device__ __forceinline__ uint32_t word_of(const uint4& r, int k) {
   return k == 0 ? r.x : k == 1 ? r.y : k == 2 ? r.z : r.w;
 }
 
-// Writes dims [8 bd, 8 bd + 8) of four consecutive keys (r0..r3, eight 16-bit
-// MFMA inputs each) into the V^T tile: dim e of the four keys becomes one
-// 8-byte row segment at dst + e * vstride (two v_perm_b32 per segment).
-__device__ __forceinline__ void store_vt4(uint16_t* dst, int vstride, const uint4& r0, const uint4& r1,
-                                          const uint4& r2, const uint4& r3) {
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-    const uint32_t w0 = __builtin_amdgcn_perm(word_of(r1, e >> 1), word_of(r0, e >> 1), sel);
-    const uint32_t w1 = __builtin_amdgcn_perm(word_of(r3, e >> 1), word_of(r2, e >> 1), sel);
-    *reinterpret_cast<uint2*>(dst + e * vstride) = uint2{w0, w1};
-  }
-}
-
 // ------------------------------------------------------------ feature capture
 // Arithmetic of the selector features (the same operation sequences as the
 // standalone prototype kernels, so the results agree bit for bit; no FP
@@ -548,15 +541,15 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
   static_assert(!PROD || TIn::bytes == 2, "the producer form stages 16-bit K/V");
   constexpr int NTHR = WAVES * 64;
   constexpr int KSTR = D + 8;        // K tile row stride, 16-bit elements (16 B pad)
-  constexpr int VSTR = kBlock + 8;   // V^T tile row stride
+  // V tile row stride: rows start 16 banks apart, so the 8 rows x 64 bytes
+  // a transposing read touches fall in distinct banks per half-wave.
+  constexpr int VSTR = D + 32;
   constexpr int KTILE = kBlock * KSTR;
-  constexpr int VTILE = D * VSTR;
+  constexpr int VTILE = kBlock * VSTR;
   constexpr int BUF = KTILE + VTILE;
   constexpr int KROWCH = D / 8;                  // 8-element chunks per K row
   constexpr int KCHUNKS = kBlock * KROWCH;
   constexpr int KCH = (KCHUNKS + NTHR - 1) / NTHR;
-  constexpr int VTASKS = (kBlock / 4) * (D / 8);  // 4 keys x 8 dims per task
-  constexpr int VTK = (VTASKS + NTHR - 1) / NTHR;
   constexpr int DT = D / 32;  // 32-row tiles of O^T
   constexpr int KS = D / 16;  // k-steps of S^T
   constexpr int EB = TIn::bytes;
@@ -663,17 +656,17 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     koff[i] = c < KCHUNKS ? key * krs + dc * 8 * EB : kOutOfRange;
     klds[i] = key * KSTR + dc * 8;
   }
-  int voff[VTK], vlds[VTK];
+  int voff[KCH], vlds[KCH];
 #pragma unroll
-  for (int i = 0; i < VTK; ++i) {
-    const int t = tid + i * NTHR;
-    const int a = t & 15, bd = t >> 4;
-    voff[i] = t < VTASKS ? 4 * a * vrs + bd * 8 * EB : kOutOfRange;
-    vlds[i] = 8 * bd * VSTR + vt_pos(4 * a);
+  for (int i = 0; i < KCH; ++i) {
+    const int c = tid + i * NTHR;
+    const int key = c / KROWCH, dc = c % KROWCH;
+    voff[i] = c < KCHUNKS ? key * vrs + dc * 8 * EB : kOutOfRange;
+    vlds[i] = key * VSTR + dc * 8;
   }
 
   raw8_t<TIn> kst[KCH];
-  raw8_t<TIn> vst[VTK][4];
+  raw8_t<TIn> vst[KCH];
 
   auto load_block = [&](int blk) {
     const int t0 = blk * kBlock;
@@ -684,27 +677,17 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
 #pragma unroll
     for (int i = 0; i < KCH; ++i) kst[i] = buf_load8<TIn>(rk, koff[i]);
 #pragma unroll
-    for (int i = 0; i < VTK; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) vst[i][j] = buf_load8<TIn>(rv, voff[i] + j * vrs);
+    for (int i = 0; i < KCH; ++i) vst[i] = buf_load8<TIn>(rv, voff[i]);
   };
 
   auto store_block = [&](int buf) {
     uint16_t* Ks = smem + buf * BUF;
-    uint16_t* Vt = Ks + KTILE;
+    uint16_t* Vs = Ks + KTILE;
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
-      if ((KCHUNKS % NTHR) == 0 || tid + i * NTHR < KCHUNKS)
+      if ((KCHUNKS % NTHR) == 0 || tid + i * NTHR < KCHUNKS) {
         *reinterpret_cast<uint4*>(Ks + klds[i]) = raw_to_mfma<TIn, F16>(kst[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < VTK; ++i) {
-      if ((VTASKS % NTHR) == 0 || tid + i * NTHR < VTASKS) {
-        const uint4 r0 = raw_to_mfma<TIn, F16>(vst[i][0]);
-        const uint4 r1 = raw_to_mfma<TIn, F16>(vst[i][1]);
-        const uint4 r2 = raw_to_mfma<TIn, F16>(vst[i][2]);
-        const uint4 r3 = raw_to_mfma<TIn, F16>(vst[i][3]);
-        store_vt4(Vt + vlds[i], VSTR, r0, r1, r2, r3);
+        *reinterpret_cast<uint4*>(Vs + vlds[i]) = raw_to_mfma<TIn, F16>(vst[i]);
       }
     }
   };
@@ -712,10 +695,9 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
   // Producer form: the last wave (which owns no tile) stages every K/V block
   // alone, so the tile waves carry no staging registers or copy work.
   constexpr int PKCH = KCHUNKS / 64;  // K chunks per producer lane
-  constexpr int PVTK = VTASKS / 64;   // V tasks per producer lane
-  static_assert(KCHUNKS % 64 == 0 && VTASKS % 64 == 0, "producer lanes split the block evenly");
+  static_assert(KCHUNKS % 64 == 0, "producer lanes split the block evenly");
   raw8_t<TIn> ks8[PKCH];
-  raw8_t<TIn> vs8[PVTK][4];
+  raw8_t<TIn> vs8[PKCH];
   auto pload = [&](int blk) {
     const int t0 = blk * kBlock;
     int nk = p.T - t0;
@@ -728,25 +710,23 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
       ks8[i] = buf_load8<TIn>(rk, (c / KROWCH) * krs + (c % KROWCH) * 8 * EB);
     }
 #pragma unroll
-    for (int i = 0; i < PVTK; ++i) {
-      const int t = lane + 64 * i;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) vs8[i][j] = buf_load8<TIn>(rv, (4 * (t & 15) + j) * vrs + (t >> 4) * 8 * EB);
+    for (int i = 0; i < PKCH; ++i) {
+      const int c = lane + 64 * i;
+      vs8[i] = buf_load8<TIn>(rv, (c / KROWCH) * vrs + (c % KROWCH) * 8 * EB);
     }
   };
   auto pstore = [&](int buf) {
     uint16_t* Ks = smem + buf * BUF;
-    uint16_t* Vt = Ks + KTILE;
+    uint16_t* Vs = Ks + KTILE;
 #pragma unroll
     for (int i = 0; i < PKCH; ++i) {
       const int c = lane + 64 * i;
       *reinterpret_cast<uint4*>(Ks + (c / KROWCH) * KSTR + (c % KROWCH) * 8) = raw_to_mfma<TIn, F16>(ks8[i]);
     }
 #pragma unroll
-    for (int i = 0; i < PVTK; ++i) {
-      const int t = lane + 64 * i;
-      store_vt4(Vt + 8 * (t >> 4) * VSTR + vt_pos(4 * (t & 15)), VSTR, raw_to_mfma<TIn, F16>(vs8[i][0]),
-                raw_to_mfma<TIn, F16>(vs8[i][1]), raw_to_mfma<TIn, F16>(vs8[i][2]), raw_to_mfma<TIn, F16>(vs8[i][3]));
+    for (int i = 0; i < PKCH; ++i) {
+      const int c = lane + 64 * i;
+      *reinterpret_cast<uint4*>(Vs + (c / KROWCH) * VSTR + (c % KROWCH) * 8) = raw_to_mfma<TIn, F16>(vs8[i]);
     }
   };
   auto produce = [&](int blk, int buf) {
@@ -982,20 +962,28 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
   };
   // O^T += V^T P^T, V^T fragments interleaved like the K fragments;
   // consecutive MFMAs go to different output tiles (dt fastest), so no MFMA
-  // waits on the previous one's result.
-  auto pv = [&](const uint16_t* Vt) {
-    const uint16_t* vp = Vt + l32 * VSTR + 8 * hl;
+  // waits on the previous one's result.  The P^T fragment pk[c][h2] holds
+  // keys K0 + 4 hl + 0..3 and K0 + 8 + 4 hl + 0..3 (K0 = 32 c + 16 h2: the
+  // S^T accumulator order) for query column l32; the matching V^T fragment
+  // of d = 32 dt + l32 is two transposing reads of 4 keys each.  Source lane
+  // s of 16-lane group gr points at keys K0 + 4 (gr / 2) + s / 4 (+ 8),
+  // dims 32 dt + 16 (gr % 2) + 4 (s % 4) + 0..3.
+  const int vlane = (4 * hl + ((lane & 15) >> 2)) * VSTR + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  auto pv = [&](const uint16_t* Vs) {
+    const uint16_t* vp = Vs + vlane;
     uint4 va[DT * 4];
 #pragma unroll
     for (int i = 0; i < DT * 4; ++i) {
       const int dt = i % DT, ch = i / DT, c = ch >> 1, h2 = ch & 1;
-      va[i] = *reinterpret_cast<const uint4*>(vp + dt * 32 * VSTR + 32 * c + 16 * h2);
+      const uint16_t* a = vp + (32 * c + 16 * h2) * VSTR + 32 * dt;
+      const uint2 lo = lds_read_tr16(a), hi = lds_read_tr16(a + 8 * VSTR);
+      va[i] = uint4{lo.x, lo.y, hi.x, hi.y};
     }
-    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * kLookahead, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4 * kLookahead, 0);
 #pragma unroll
     for (int i = 0; i < DT * 4 - 2 * kLookahead; ++i) {
       __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
     }
     __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2 * kLookahead, 0);
 #pragma unroll
@@ -1121,21 +1109,16 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
     for (int e0 = 0; e0 < E; e0 += kBlock) {
       buf ^= 1;  // its last reader finished before the previous barrier
       uint16_t* Ks = smem + buf * BUF;
-      uint16_t* Vt = Ks + KTILE;
+      uint16_t* Vs = Ks + KTILE;
       for (int c = tid; c < KCHUNKS; c += NTHR) {
         const int key = c / KROWCH, dc = c % KROWCH;
         const int en = e0 + key;
         *reinterpret_cast<uint4*>(Ks + key * KSTR + dc * 8) = load_row8(p.skey, en, node_of(en), dc * 8);
       }
-      for (int t = tid; t < VTASKS; t += NTHR) {
-        const int a = t & 15, bd = t >> 4;
-        uint4 r[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int en = e0 + 4 * a + j;
-          r[j] = load_row8(p.sval, en, node_of(en), bd * 8);
-        }
-        store_vt4(Vt + 8 * bd * VSTR + vt_pos(4 * a), VSTR, r[0], r[1], r[2], r[3]);
+      for (int c = tid; c < KCHUNKS; c += NTHR) {
+        const int key = c / KROWCH, dc = c % KROWCH;
+        const int en = e0 + key;
+        *reinterpret_cast<uint4*>(Vs + key * VSTR + dc * 8) = load_row8(p.sval, en, node_of(en), dc * 8);
       }
       if (tid < kBlock) {
         const int en = e0 + tid;
