@@ -166,9 +166,13 @@ int spruce_sparse_prefill_mask(
  * with count 0 (log count -inf) and nodes < 0 or >= N add nothing.
  *   nodes        [B, Hkv, Qb, S] int32, strides ns (a layer slice of the
  *                residual_summary_nodes tensor, trailing -1 padding).
- *   sum_keys, sum_values  float32 [B, Hkv, N, P, D] contiguous (16-byte
- *                aligned), sum_log_counts float32 [B, N, P] contiguous: the
+ *   sum_keys, sum_values  [B, Hkv, N, P, D] contiguous (16-byte aligned),
+ *                sum_log_counts float32 [B, N, P] contiguous: the
  *                KVSummaryTable spruce_kv_summary writes, N tree nodes.
+ *   sum_dtype    element type of sum_keys / sum_values: SPRUCE_DTYPE_F32
+ *                (the table as written), or the 16-bit input dtype (a copy
+ *                rounded to nearest even, which the kernel stages like a key
+ *                block: same results, half the bytes and no conversion).
  * The summary keys and values are rounded to the MFMA input type (bf16, or
  * f16 for f16 inputs) like the key blocks.
  */
@@ -178,7 +182,8 @@ int spruce_sparse_prefill_index_summaries(
     const void* v, const int64_t vs[4],
     const int32_t* idx, const int64_t is[4], int64_t K,
     const int32_t* nodes, const int64_t ns[4], int64_t S,
-    const float* sum_keys, const float* sum_values, const float* sum_log_counts, int64_t N, int64_t P,
+    const void* sum_keys, const void* sum_values, const float* sum_log_counts, int sum_dtype,
+    int64_t N, int64_t P,
     int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D,
     float scale, int dtype, int variant,
     void* out, const int64_t os[4],
@@ -191,7 +196,8 @@ int spruce_sparse_prefill_index_summaries(
  * :225-229 add it to the scores).  key_valid uint8 [B, T] (batch stride kvs
  * elements, tokens contiguous): nonzero marks a real token; a key with
  * key_valid == 0 gets no weight in any row.  Pass nodes = NULL and S = 0 for
- * no residual summaries.  A query row whose causal listed keys are all
+ * no residual summaries (the summary arguments are as in
+ * spruce_sparse_prefill_index_summaries).  A query row whose causal listed keys are all
  * padding (a left-padded position) writes zeros.
  */
 int spruce_sparse_prefill_index_masked(
@@ -201,7 +207,8 @@ int spruce_sparse_prefill_index_masked(
     const int32_t* idx, const int64_t is[4], int64_t K,
     const uint8_t* key_valid, int64_t kvs,
     const int32_t* nodes, const int64_t ns[4], int64_t S,
-    const float* sum_keys, const float* sum_values, const float* sum_log_counts, int64_t N, int64_t P,
+    const void* sum_keys, const void* sum_values, const float* sum_log_counts, int sum_dtype,
+    int64_t N, int64_t P,
     int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D,
     float scale, int dtype, int variant,
     void* out, const int64_t os[4],

@@ -90,13 +90,14 @@ struct AttnParams {
   int amask_dtype, amask_heads, amask_vec, amask_rows16, amask_tk;
   float amask_mul;
   // residual summaries (sparse/attention.py:226-265): per row, nodes
-  // [B, Hkv, Qb, S] int32 (-1 = none); table keys/values float32
-  // [B, Hkv, N, P, D] and natural-log counts [B, N, P], all contiguous.
+  // [B, Hkv, Qb, S] int32 (-1 = none); table keys/values [B, Hkv, N, P, D]
+  // (float32, or already rounded to the MFMA input type when sum16) and
+  // natural-log counts [B, N, P] float32, all contiguous.
   const int32_t* snode;
   int64_t sns[4];
-  int S, N, P;
-  const float* skey;
-  const float* sval;
+  int S, N, P, sum16;
+  const void* skey;
+  const void* sval;
   const float* slog;
   float sbias;  // log counts -> raw score units: log2(e) / cs
   int tpp;  // tiles per part: waves 0..tpp-1 of a workgroup own a tile
@@ -1013,16 +1014,88 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
   };
   auto vbits = [&](uint32_t raw) -> uint64_t { return KVAL ? __ballot(raw != 0u) : ~0ull; };
 
+  // ---- residual summaries of the row (SUMM): entry e is prototype e % P
+  // of the row's (e / P)-th node, appended after the exact keys as chunks of
+  // 64 keys (sparse/attention.py:232-265).  Missing nodes and empty
+  // prototypes get a -inf bias, so they add exactly zero weight.
+  __shared__ __attribute__((aligned(16))) float sbias[SUMM ? 2 : 1][kBlock];
+  const int32_t* nrow =
+      SUMM ? p.snode + (int64_t)b * p.sns[0] + (int64_t)g * p.sns[1] + (int64_t)qb * p.sns[2] : nullptr;
+  // The row's summary entries: listed nodes (up to the last valid one) x P.
+  auto summary_entries = [&]() __attribute__((always_inline)) {
+    int nn = 0;  // one past the last listed node (uniform)
+    for (int j0 = 0; j0 < p.S; j0 += 64) {
+      const int j = j0 + lane;
+      const int v = j < p.S ? nrow[(int64_t)j * p.sns[3]] : -1;
+      const uint64_t m = __ballot(v >= 0 && v < p.N);
+      if (m) nn = j0 + 64 - __builtin_clzll(m);
+    }
+    return nn * p.P;
+  };
+  const int64_t bg = (int64_t)b * p.Hkv + g;
+  auto node_of = [&](int en, int E) __attribute__((always_inline)) {
+    if (en >= E) return -1;
+    const int v = nrow[(int64_t)(en / p.P) * p.sns[3]];
+    return (v >= 0 && v < p.N) ? v : -1;
+  };
+  // Table row offset (elements) of entry en of node `node`, dims d0..
+  auto row_at = [&](int en, int node, int d0) __attribute__((always_inline)) { return ((bg * p.N + node) * p.P + en % p.P) * (int64_t)D + d0; };
+  auto load_row8 = [&](const void* base, int en, int node, int d0) __attribute__((always_inline)) {
+    if (node < 0) return uint4{0u, 0u, 0u, 0u};
+    if (EB == 2 && p.sum16)  // a copy in the input type (never for float32 inputs)
+      return *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + row_at(en, node, d0));
+    const float4* s = reinterpret_cast<const float4*>(static_cast<const float*>(base) + row_at(en, node, d0));
+    const float4 x = s[0], y = s[1];
+    return uint4{pack2<F16>(x.x, x.y), pack2<F16>(x.z, x.w), pack2<F16>(y.x, y.y), pack2<F16>(y.z, y.w)};
+  };
+  // Producer form: the producer wave stages each chunk while the tile waves
+  // compute the previous one (the first chunk while they compute the row's
+  // last key block), with the key blocks' barrier sequence.  Lane l holds
+  // the node of entry e0 + l; the 16-byte pieces of the 64 table rows are
+  // spread over the lanes as in the key blocks' staging, each taking its
+  // entry's node from the owning lane.  A 16-bit copy of the table is staged
+  // with all of a chunk's loads in flight at once (the producer returns
+  // after the output barrier, so none of the tile waves' registers are live
+  // here); a float32 table in batches of kSumBatch pieces per lane (2
+  // float4 loads each), rounded on the way.
+  constexpr int kSumBatch = PKCH / 2;
+  auto stage_rows = [&](const void* table, uint16_t* dst, int stride, int e0, int mine) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i0 = 0; i0 < PKCH; i0 += kSumBatch) {
+      float4 x[2 * kSumBatch];
+#pragma unroll
+      for (int i = 0; i < kSumBatch; ++i) {
+        const int c = lane + 64 * (i0 + i), key = c / KROWCH, dc = c % KROWCH;
+        const int node = __shfl(mine, key);
+        if (node >= 0) {
+          const float4* src =
+              reinterpret_cast<const float4*>(static_cast<const float*>(table) + row_at(e0 + key, node, dc * 8));
+          x[2 * i] = src[0];
+          x[2 * i + 1] = src[1];
+        } else {
+          x[2 * i] = x[2 * i + 1] = float4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kSumBatch; ++i) {
+        const int c = lane + 64 * (i0 + i), key = c / KROWCH, dc = c % KROWCH;
+        const float4 u = x[2 * i], w = x[2 * i + 1];
+        *reinterpret_cast<uint4*>(dst + key * stride + dc * 8) =
+            uint4{pack2<F16>(u.x, u.y), pack2<F16>(u.z, u.w), pack2<F16>(w.x, w.y), pack2<F16>(w.z, w.w)};
+      }
+    }
+  };
   BlockIter<MODE> it;
   it.init(p, b, g, qb, part, hq, lane, half_major);
   int cur_id = 0;
   bool cur_en = false;
   int buf = 0;
-  if (it.next(cur_id, cur_en)) {
-    if constexpr (PROD) {
-      // Same barrier sequence on both sides: one before the first block and
-      // one between consecutive blocks.
-      if (wave == WAVES - 1) {
+  const bool any_block = it.next(cur_id, cur_en);
+  if constexpr (PROD) {
+    // Same barrier sequence on both sides: one before the first block and
+    // one between consecutive blocks.
+    if (wave == WAVES - 1) {
+      if (any_block) {
         produce(cur_id, 0);
         __syncthreads();
         while (true) {
@@ -1033,41 +1106,56 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
           __syncthreads();
           buf ^= 1;
         }
-      } else {
-        if (!q_ready) convert_q();
-        uint32_t vcur = vbyte(cur_id);
-        fetch_amask(cur_id);
-        __syncthreads();
-        while (true) {
-          int nid = 0;
-          bool nen = false;
-          const bool more = it.next(nid, nen);
-          const uint32_t vnext = more ? vbyte(nid) : 0u;
-          if (active && cur_en) compute(buf, cur_id == qb, nullptr, vbits(vcur), more ? nid : -1);
-          if (!more) break;
-          __syncthreads();
-          buf ^= 1;
-          cur_id = nid;
-          cur_en = nen;
-          vcur = vnext;
-        }
       }
-    } else {
-      uint32_t vcur = vbyte(cur_id);
-      load_block(cur_id);
-      fetch_amask(cur_id);
+      if constexpr (SUMM) {
+        const int E = summary_entries();
+        int mine = node_of(lane, E);  // lane l: the node of entry e0 + l
+        for (int e0 = 0; e0 < E; e0 += kBlock) {
+          buf ^= 1;  // its last readers finished before the previous barrier
+          uint16_t* Ks = smem + buf * BUF;
+          const int next = node_of(e0 + kBlock + lane, E);  // the next chunk's, read ahead
+          sbias[buf][lane] =
+              mine < 0 ? -INFINITY : p.slog[((int64_t)b * p.N + mine) * p.P + (e0 + lane) % p.P] * p.sbias;
+          if (p.sum16) {
+            uint4 xk[PKCH], xv[PKCH];
+#pragma unroll
+            for (int i = 0; i < PKCH; ++i) {
+              const int c = lane + 64 * i, key = c / KROWCH, dc = c % KROWCH;
+              const int node = __shfl(mine, key);
+              const int64_t off = node >= 0 ? row_at(e0 + key, node, dc * 8) : 0;
+              xk[i] = node >= 0 ? *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.skey) + off)
+                                : uint4{0u, 0u, 0u, 0u};
+              xv[i] = node >= 0 ? *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.sval) + off)
+                                : uint4{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int i = 0; i < PKCH; ++i) {
+              const int c = lane + 64 * i, key = c / KROWCH, dc = c % KROWCH;
+              *reinterpret_cast<uint4*>(Ks + key * KSTR + dc * 8) = xk[i];
+              *reinterpret_cast<uint4*>(Ks + KTILE + key * VSTR + dc * 8) = xv[i];
+            }
+          } else {
+            stage_rows(p.skey, Ks, KSTR, e0, mine);
+            stage_rows(p.sval, Ks + KTILE, VSTR, e0, mine);
+          }
+          __syncthreads();
+          mine = next;
+        }
+        __syncthreads();  // the output staging's barrier below
+        return;
+      }
+    } else if (any_block) {
       if (!q_ready) convert_q();
-      store_block(0);
+      uint32_t vcur = vbyte(cur_id);
+      fetch_amask(cur_id);
       __syncthreads();
       while (true) {
         int nid = 0;
         bool nen = false;
         const bool more = it.next(nid, nen);
         const uint32_t vnext = more ? vbyte(nid) : 0u;
-        if (more) load_block(nid);
         if (active && cur_en) compute(buf, cur_id == qb, nullptr, vbits(vcur), more ? nid : -1);
         if (!more) break;
-        store_block(buf ^ 1);
         __syncthreads();
         buf ^= 1;
         cur_id = nid;
@@ -1075,58 +1163,63 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
         vcur = vnext;
       }
     }
+  } else if (any_block) {
+    uint32_t vcur = vbyte(cur_id);
+    load_block(cur_id);
+    fetch_amask(cur_id);
+    if (!q_ready) convert_q();
+    store_block(0);
+    __syncthreads();
+    while (true) {
+      int nid = 0;
+      bool nen = false;
+      const bool more = it.next(nid, nen);
+      const uint32_t vnext = more ? vbyte(nid) : 0u;
+      if (more) load_block(nid);
+      if (active && cur_en) compute(buf, cur_id == qb, nullptr, vbits(vcur), more ? nid : -1);
+      if (!more) break;
+      store_block(buf ^ 1);
+      __syncthreads();
+      buf ^= 1;
+      cur_id = nid;
+      cur_en = nen;
+      vcur = vnext;
+    }
   }
 
   if constexpr (SUMM) {
-    // Residual summaries of the row: entry e is prototype e % P of the
-    // row's (e / P)-th node, appended after the exact keys as chunks of 64
-    // keys (sparse/attention.py:232-265).  Missing nodes and empty prototypes
-    // get a -inf bias, so they add exactly zero weight.
-    __shared__ __attribute__((aligned(16))) float sbias[2][kBlock];
-    const int32_t* nrow = p.snode + (int64_t)b * p.sns[0] + (int64_t)g * p.sns[1] + (int64_t)qb * p.sns[2];
-    int nn = 0;  // one past the last listed node (uniform)
-    for (int j0 = 0; j0 < p.S; j0 += 64) {
-      const int j = j0 + lane;
-      const int v = j < p.S ? nrow[(int64_t)j * p.sns[3]] : -1;
-      const uint64_t m = __ballot(v >= 0 && v < p.N);
-      if (m) nn = j0 + 64 - __builtin_clzll(m);
-    }
-    const int E = nn * p.P;
+    const int E = summary_entries();
     if (E > 0 && !q_ready) convert_q();  // the row listed no exact block
-    const int64_t bg = (int64_t)b * p.Hkv + g;
-    auto node_of = [&](int en) {
-      if (en >= E) return -1;
-      const int v = nrow[(int64_t)(en / p.P) * p.sns[3]];
-      return (v >= 0 && v < p.N) ? v : -1;
-    };
-    auto load_row8 = [&](const float* base, int en, int node, int d0) {
-      if (node < 0) return uint4{0u, 0u, 0u, 0u};
-      const float4* s = reinterpret_cast<const float4*>(
-          base + ((bg * p.N + node) * p.P + en % p.P) * (int64_t)D + d0);
-      const float4 x = s[0], y = s[1];
-      return uint4{pack2<F16>(x.x, x.y), pack2<F16>(x.z, x.w), pack2<F16>(y.x, y.y), pack2<F16>(y.z, y.w)};
-    };
-    for (int e0 = 0; e0 < E; e0 += kBlock) {
-      buf ^= 1;  // its last reader finished before the previous barrier
-      uint16_t* Ks = smem + buf * BUF;
-      uint16_t* Vs = Ks + KTILE;
-      for (int c = tid; c < KCHUNKS; c += NTHR) {
-        const int key = c / KROWCH, dc = c % KROWCH;
-        const int en = e0 + key;
-        *reinterpret_cast<uint4*>(Ks + key * KSTR + dc * 8) = load_row8(p.skey, en, node_of(en), dc * 8);
+    if constexpr (PROD) {
+      // The tile waves' side of produce_summaries (the producer returned).
+      for (int e0 = 0; e0 < E; e0 += kBlock) {
+        buf ^= 1;
+        __syncthreads();
+        if (active) compute(buf, false, sbias[buf], ~0ull, -1);
       }
-      for (int c = tid; c < KCHUNKS; c += NTHR) {
-        const int key = c / KROWCH, dc = c % KROWCH;
-        const int en = e0 + key;
-        *reinterpret_cast<uint4*>(Vs + key * VSTR + dc * 8) = load_row8(p.sval, en, node_of(en), dc * 8);
+    } else {
+      for (int e0 = 0; e0 < E; e0 += kBlock) {
+        buf ^= 1;  // its last reader finished before the previous barrier
+        uint16_t* Ks = smem + buf * BUF;
+        uint16_t* Vs = Ks + KTILE;
+        for (int c = tid; c < KCHUNKS; c += NTHR) {
+          const int key = c / KROWCH, dc = c % KROWCH;
+          const int en = e0 + key;
+          *reinterpret_cast<uint4*>(Ks + key * KSTR + dc * 8) = load_row8(p.skey, en, node_of(en, E), dc * 8);
+        }
+        for (int c = tid; c < KCHUNKS; c += NTHR) {
+          const int key = c / KROWCH, dc = c % KROWCH;
+          const int en = e0 + key;
+          *reinterpret_cast<uint4*>(Vs + key * VSTR + dc * 8) = load_row8(p.sval, en, node_of(en, E), dc * 8);
+        }
+        if (tid < kBlock) {
+          const int en = e0 + tid;
+          const int node = node_of(en, E);
+          sbias[buf][tid] = node < 0 ? -INFINITY : p.slog[((int64_t)b * p.N + node) * p.P + en % p.P] * p.sbias;
+        }
+        __syncthreads();
+        if (active) compute(buf, false, sbias[buf], ~0ull, -1);
       }
-      if (tid < kBlock) {
-        const int en = e0 + tid;
-        const int node = node_of(en);
-        sbias[buf][tid] = node < 0 ? -INFINITY : p.slog[((int64_t)b * p.N + node) * p.P + en % p.P] * p.sbias;
-      }
-      __syncthreads();
-      if (active) compute(buf, false, sbias[buf], ~0ull, -1);
     }
   }
 

@@ -135,7 +135,8 @@ def direct_index_sparse_prefill(q, k, v, indices, scale, block_size=64,
                 spruce_hip.ptr(k), spruce_hip.strides(k),
                 spruce_hip.ptr(v), spruce_hip.strides(v),
                 spruce_hip.ptr(indices), spruce_hip.strides(indices), indices.shape[3],
-                spruce_hip.ptr(kv8), T, None, zero4, 0, None, None, None, 0, 1,
+                spruce_hip.ptr(kv8), T, None, zero4, 0, None, None, None,
+                spruce_hip.DTYPE_CODES[torch.float32], 0, 1,
                 B, Hq, Hkv, T, D, float(scale), spruce_hip.dtype_code(q),
                 spruce_hip.variant_code(kernel_variant),
                 spruce_hip.ptr(out), out_strides, spruce_hip.stream_of(q))
@@ -186,6 +187,11 @@ def direct_index_sparse_summaries(q, k, v, indices, nodes, table, scale, block_s
         raise ValueError("q, k, v, indices and nodes must have a contiguous final dimension")
     if any(t.device != q.device for t in (indices, nodes, keys, values, logc)):
         raise ValueError("indices, nodes and the summary table must be on the same device as q")
+    if q.dtype != torch.float32:
+        # The kernel rounds the table to the 16-bit input type anyway; a
+        # rounded copy (round to nearest even, as the kernel rounds) halves
+        # the bytes its producer stages per summary chunk.
+        keys, values = keys.to(q.dtype), values.to(q.dtype)
     out, out_strides = _output(q)
     if key_valid is not None:
         kv8 = _key_valid(key_valid, B, T, q.device)
@@ -198,7 +204,7 @@ def direct_index_sparse_summaries(q, k, v, indices, nodes, table, scale, block_s
                 spruce_hip.ptr(kv8), T,
                 spruce_hip.ptr(nodes), spruce_hip.strides(nodes), nodes.shape[3],
                 spruce_hip.ptr(keys), spruce_hip.ptr(values), spruce_hip.ptr(logc),
-                keys.shape[2], keys.shape[3],
+                spruce_hip.dtype_code(keys), keys.shape[2], keys.shape[3],
                 B, Hq, Hkv, T, D, float(scale), spruce_hip.dtype_code(q),
                 spruce_hip.variant_code(kernel_variant),
                 spruce_hip.ptr(out), out_strides, spruce_hip.stream_of(q))
@@ -213,7 +219,7 @@ def direct_index_sparse_summaries(q, k, v, indices, nodes, table, scale, block_s
             spruce_hip.ptr(indices), spruce_hip.strides(indices), indices.shape[3],
             spruce_hip.ptr(nodes), spruce_hip.strides(nodes), nodes.shape[3],
             spruce_hip.ptr(keys), spruce_hip.ptr(values), spruce_hip.ptr(logc),
-            keys.shape[2], keys.shape[3],
+            spruce_hip.dtype_code(keys), keys.shape[2], keys.shape[3],
             B, Hq, Hkv, T, D, float(scale), spruce_hip.dtype_code(q),
             spruce_hip.variant_code(kernel_variant),
             spruce_hip.ptr(out), out_strides, spruce_hip.stream_of(q))

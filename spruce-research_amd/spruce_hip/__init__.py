@@ -77,7 +77,7 @@ _SIGNATURES = {
     "spruce_group_avg_tokens": [_p, _STRIDES, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _p],
     "spruce_sparse_prefill_index_summaries": [
         _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _i64,
-        _p, _STRIDES, _i64, _p, _p, _p, _i64, _i64,
+        _p, _STRIDES, _i64, _p, _p, _p, ctypes.c_int, _i64, _i64,
         _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int, ctypes.c_int,
         _p, _STRIDES, _p],
     "spruce_sparse_prefill_index_amask": [
@@ -86,7 +86,7 @@ _SIGNATURES = {
         _p, _STRIDES, _p],
     "spruce_sparse_prefill_index_masked": [
         _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _p, _STRIDES, _i64, _p, _i64,
-        _p, _STRIDES, _i64, _p, _p, _p, _i64, _i64,
+        _p, _STRIDES, _i64, _p, _p, _p, ctypes.c_int, _i64, _i64,
         _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int, ctypes.c_int,
         _p, _STRIDES, _p],
     "spruce_residual_frontier": [_p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p],
