@@ -183,3 +183,20 @@ def test_attention_mask_validation_before_launch():
     for kwargs, message in cases:
         assert call(**kwargs) == -1, kwargs
         assert message in spruce_hip.last_error(), (kwargs, spruce_hip.last_error())
+
+
+def test_summary_table_dtype_validation_before_launch():
+    # The summary table is float32 or a copy in the 16-bit input dtype.
+    lib = spruce_hip.lib()
+    fake = ctypes.c_void_p(1 << 20)
+    st = _strides(0, 0, 128, 1)
+
+    def call(dtype, sum_dtype):
+        return lib.spruce_sparse_prefill_index_summaries(
+            fake, st, fake, st, fake, st, fake, _strides(0, 0, 1, 1), 1,
+            fake, _strides(0, 0, 1, 1), 1, fake, fake, fake, sum_dtype, 3, 1,
+            1, 4, 2, 64, 128, 0.1, dtype, 0, fake, _strides(0, 128, 512, 1), None)
+
+    for dtype, sum_dtype in ((0, 1), (1, 0), (2, 0), (0, 7)):
+        assert call(dtype, sum_dtype) == -1, (dtype, sum_dtype)
+        assert "float32 or the 16-bit input dtype" in spruce_hip.last_error(), spruce_hip.last_error()
