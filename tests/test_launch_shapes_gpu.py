@@ -14,10 +14,15 @@ import pytest
 import torch
 
 import oracle.attention as ora
-from interfaces.residual_summaries import build_residual_summary_nodes
+from interfaces.residual_summaries import build_residual_summary_nodes, build_residual_tree_layout
 from kernels.block_mask import block_sparse_prefill
-from kernels.direct_index import direct_index_sparse_csr, direct_index_sparse_prefill
+from kernels.direct_index import (
+    direct_index_sparse_csr,
+    direct_index_sparse_prefill,
+    direct_index_sparse_summaries,
+)
 from sparse.attention import sparse_prefill_attention_forward
+from sparse.summaries import build_kv_summary_table
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -65,10 +70,10 @@ def _alone_and_first(call, inputs):
 
 @pytest.mark.parametrize("Hq,Hkv,B,dtype", SHAPES)
 @pytest.mark.parametrize("entry", ["index", "key_valid", "attn_mask", "csr", "block_mask",
-                                   "summaries"])
+                                   "summaries", "summaries_key_valid"])
 def test_split_and_unsplit_launches_agree(entry, Hq, Hkv, B, dtype):
     print(f"launch shapes: {entry} Hq={Hq} Hkv={Hkv} B={B} {dtype}", flush=True)
-    if entry == "summaries" and dtype == torch.float32:
+    if entry.startswith("summaries") and dtype == torch.float32:
         pytest.skip("summary keys are covered in 16-bit; fp32 runs the same non-producer forms")
     rng = np.random.default_rng(Hq * 100 + B)
     q, k, v = _qkv(Hq + B, B, Hq, Hkv, dtype)
@@ -107,6 +112,18 @@ def test_split_and_unsplit_launches_agree(entry, Hq, Hkv, B, dtype):
         mask |= torch.eye(QB, dtype=torch.bool, device=DEV)
         alone, first = _alone_and_first(lambda q, k, v, m: block_sparse_prefill(q, k, v, m, scale),
                                         (q, k, v, mask))
+    elif entry == "summaries_key_valid":
+        # The key-padding entry with summaries: the layer's table is built per
+        # batch element, so batch element 0's table is the same alone.
+        lengths = torch.tensor(rng.integers(T // 2, T + 1, size=B))
+        kv = (torch.arange(T)[None] < lengths[:, None]).to(DEV)
+        nodes = build_residual_summary_nodes(idx[:, None])[:, 0].to(torch.int32).contiguous()
+        lay = build_residual_tree_layout(QB)
+
+        def call(q, k, v, i, n, m):
+            table = build_kv_summary_table(k, v, lay, block_size=64, prototypes=2, token_mask=m)
+            return direct_index_sparse_summaries(q, k, v, i, n, table, scale, key_valid=m)
+        alone, first = _alone_and_first(call, (q, k, v, idx, nodes, kv))
     else:
         selected = idx[:, None]                          # [B, 1, Hkv, QB, K]
         residual = build_residual_summary_nodes(selected)
