@@ -143,6 +143,12 @@ __device__ __forceinline__ uint32_t elem16(const uint4& r, int e) {
 // i / 4 + 4 j points at.  Two reads give a lane the 8 keys of its MFMA
 // k-positions for one d.
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
+// 16 bytes per lane from a buffer straight into LDS: lane l's bytes land at
+// lds + 16 l (buffer_load_dwordx4 ... lds, base in M0); out-of-range
+// offsets write zeros.
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t r, void* lds, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+}
 __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
   const v4i16_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (__attribute__((address_space(3))) v4i16_t*)(const_cast<uint16_t*>(p)));
@@ -694,45 +700,43 @@ __global__ __launch_bounds__(WAVES * 64) void sparse_prefill_kernel(const AttnPa
   };
 
   // Producer form: the last wave (which owns no tile) stages every K/V block
-  // alone, so the tile waves carry no staging registers or copy work.
-  constexpr int PKCH = KCHUNKS / 64;  // K chunks per producer lane
+  // alone, so the tile waves carry no staging registers or copy work.  It
+  // stages by loads straight into LDS (buffer_load ... lds: lane l of an
+  // instruction writes LDS bytes [16 l, 16 l + 16) after the M0 base): the
+  // tiles' padded rows are covered granule by granule, each lane fetching
+  // the 16 K/V bytes that belong at its granule, and the pad granules read
+  // out of range (zeros, no memory traffic).  The barrier after a block
+  // waits for these loads (vmcnt), as it waited for the register copies.
+  constexpr int PKCH = KCHUNKS / 64;  // K chunks per lane of one wave (summary chunks)
   static_assert(KCHUNKS % 64 == 0, "producer lanes split the block evenly");
-  raw8_t<TIn> ks8[PKCH];
-  raw8_t<TIn> vs8[PKCH];
-  auto pload = [&](int blk) {
-    const int t0 = blk * kBlock;
-    int nk = p.T - t0;
-    nk = nk > kBlock ? kBlock : nk;
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + (int64_t)t0 * krs, (uint32_t)(nk * krs));
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + (int64_t)t0 * vrs, (uint32_t)(nk * vrs));
-#pragma unroll
-    for (int i = 0; i < PKCH; ++i) {
-      const int c = lane + 64 * i;
-      ks8[i] = buf_load8<TIn>(rk, (c / KROWCH) * krs + (c % KROWCH) * 8 * EB);
-    }
-#pragma unroll
-    for (int i = 0; i < PKCH; ++i) {
-      const int c = lane + 64 * i;
-      vs8[i] = buf_load8<TIn>(rv, (c / KROWCH) * vrs + (c % KROWCH) * 8 * EB);
-    }
+  constexpr int KG = KSTR / 8, VG = VSTR / 8;  // 16-byte granules per LDS row, data and pad
+  static_assert(KSTR % 8 == 0 && VSTR % 8 == 0, "tile rows are whole 16-byte granules");
+  auto dma_off = [&](int i, int G, int rs) {
+    const int gidx = 64 * i + lane, row = gidx / G, col = gidx - row * G;
+    return col < KROWCH ? row * rs + col * 16 : kOutOfRange;
   };
-  auto pstore = [&](int buf) {
-    uint16_t* Ks = smem + buf * BUF;
-    uint16_t* Vs = Ks + KTILE;
+  int kdma[PROD ? KG : 1], vdma[PROD ? VG : 1];  // this lane's offsets, the same for every block
+  if constexpr (PROD) {
 #pragma unroll
-    for (int i = 0; i < PKCH; ++i) {
-      const int c = lane + 64 * i;
-      *reinterpret_cast<uint4*>(Ks + (c / KROWCH) * KSTR + (c % KROWCH) * 8) = raw_to_mfma<TIn, F16>(ks8[i]);
-    }
+    for (int i = 0; i < KG; ++i) kdma[i] = dma_off(i, KG, krs);
 #pragma unroll
-    for (int i = 0; i < PKCH; ++i) {
-      const int c = lane + 64 * i;
-      *reinterpret_cast<uint4*>(Vs + (c / KROWCH) * VSTR + (c % KROWCH) * 8) = raw_to_mfma<TIn, F16>(vs8[i]);
-    }
-  };
+    for (int i = 0; i < VG; ++i) vdma[i] = dma_off(i, VG, vrs);
+  }
   auto produce = [&](int blk, int buf) {
-    pload(blk);
-    pstore(buf);
+    if constexpr (EB == 2) {
+      const int t0 = blk * kBlock;
+      int nk = p.T - t0;
+      nk = nk > kBlock ? kBlock : nk;
+      const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + (int64_t)t0 * krs, (uint32_t)(nk * krs));
+      const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase + (int64_t)t0 * vrs, (uint32_t)(nk * vrs));
+      uint16_t* Ks = smem + buf * BUF;
+#pragma unroll
+      for (int i = 0; i < KG; ++i)
+        buffer_load_lds16(rk, Ks + 512 * i, kdma[i]);
+#pragma unroll
+      for (int i = 0; i < VG; ++i)
+        buffer_load_lds16(rv, Ks + KTILE + 512 * i, vdma[i]);
+    }
   };
 
   float m_use = -INFINITY;  // softmax reference point (scaled, log2 domain)
