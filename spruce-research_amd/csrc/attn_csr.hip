@@ -15,8 +15,9 @@ extern "C" int spruce_sparse_prefill_csr(
                              shape);
   if (rc) return rc;
   split_small_grid(p, shape, variant);
-  SPRUCE_REQUIRE(indptr != nullptr && indices != nullptr, "indptr and indices must be non-null");
   SPRUCE_REQUIRE(nnz >= 0 && nnz < ((int64_t)1 << 31), "invalid nnz %lld", (long long)nnz);
+  // With no entries (every row empty) indices is never read and may be null.
+  SPRUCE_REQUIRE(indptr != nullptr && (indices != nullptr || nnz == 0), "indptr and indices must be non-null");
   p.indptr = indptr;
   p.nnz = (int)nnz;
   p.indices = indices;

@@ -172,6 +172,20 @@ def test_csr_rows_with_row_order_and_empty_rows():
     assert torch.equal(plain, ordered)
 
 
+@pytest.mark.parametrize("T", [1, 100])
+def test_csr_with_no_entries_writes_zeros(T):
+    # Every row empty: nnz = 0 and an empty (null) indices tensor.
+    gen = torch.Generator().manual_seed(T)
+    dev = [_bthd(2, T, H, 64, torch.bfloat16, gen).transpose(1, 2).contiguous().to(DEV).transpose(1, 2)
+           for H in (4, 2, 2)]
+    rows = 2 * 2 * ((T + 63) // 64)
+    indptr = torch.zeros(rows + 1, dtype=torch.int32, device=DEV)
+    indices = torch.zeros(0, dtype=torch.int32, device=DEV)
+    out = direct_index_sparse_csr(*dev, indptr, indices, scale=0.125)
+    torch.cuda.synchronize()
+    assert out.shape == (2, T, 4, 64) and not out.float().abs().any()
+
+
 def test_mask_per_query_head_and_per_kv_head():
     rng = np.random.default_rng(31)
     B, Hq, Hkv, T, D = 1, 8, 2, 512, 128
