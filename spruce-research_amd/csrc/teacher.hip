@@ -286,14 +286,51 @@ __global__ __launch_bounds__(WAVES * 64) void block_mass_kernel(const MassParams
     }
   };
 
-  load_k(0);
-  store_k(0);
+  // With a wave that owns no tile (G = 3, 5, 6, 7 in 8-wave parts) and
+  // 16-bit inputs, that wave stages every K block alone by loads straight
+  // into LDS (17 buffer loads for the tile's padded rows, the pad granules
+  // out of range) and the tile waves only compute; both sides keep the same
+  // barrier sequence, and the producer leaves after the last block (no
+  // barrier follows the loop).
+  constexpr int KG = KSTR / 8;  // 16-byte granules per LDS row, data and pad
+  const bool producer_form = EB == 2 && p.tpp < WAVES;
+  if (producer_form && wave == WAVES - 1) {
+    if constexpr (EB == 2) {
+      int kdma[KG];
+#pragma unroll
+      for (int i = 0; i < KG; ++i) {
+        const int gidx = 64 * i + lane, row = gidx / KG, col = gidx - row * KG;
+        kdma[i] = col < KROWCH ? row * krs + col * 16 : kOutOfRange;
+      }
+      auto stage = [&](int blk, int sbuf) {
+        int nk = p.T - blk * kBlock;
+        nk = nk > kBlock ? kBlock : nk;
+        const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase + (int64_t)blk * kBlock * krs, (uint32_t)(nk * krs));
+        uint16_t* Ks = smem + sbuf * KTILE;
+#pragma unroll
+        for (int i = 0; i < KG; ++i) buffer_load_lds16(rk, Ks + 512 * i, kdma[i]);
+      };
+      stage(0, 0);
+      __syncthreads();
+      int pbuf = 0;
+      for (int J = 0; J < qb; ++J) {
+        stage(J + 1, pbuf ^ 1);
+        __syncthreads();
+        pbuf ^= 1;
+      }
+    }
+    return;
+  }
+  if (!producer_form) {
+    load_k(0);
+    store_k(0);
+  }
   __syncthreads();
   int buf = 0;
   for (int J = 0; J < qb; ++J) {
-    load_k(J + 1);
+    if (!producer_form) load_k(J + 1);
     if (active) step(std::false_type{}, J, buf);
-    store_k(buf ^ 1);
+    if (!producer_form) store_k(buf ^ 1);
     __syncthreads();
     buf ^= 1;
   }
