@@ -343,6 +343,29 @@ int spruce_causal_topk(const float* scores, int64_t R, int64_t Qb, int64_t Kb, i
                        void* stream);
 
 /*
+ * The whole flat selector in two launches: the reference's flat route
+ * (scripts/eval_gate.py:70-72) -- pooled block features
+ * (teacher/chunked_extract.py:27-80), FlatGate MaxSim scoring
+ * (selector/gate.py:29-101), causal mask and top-k (selector/recall.py:26-35,
+ * ties per selector/baselines.py:59-62) -- with the selected blocks identical
+ * to spruce_selector_pool -> spruce_gate_project2 -> spruce_gate_scores ->
+ * spruce_causal_topk on the same inputs.
+ *   q [B, Hq, T, 128], k [B, Hkv, T, 128] (any strides, contiguous last dim,
+ *   16-byte aligned rows), bf16 or f16; wq, wk [128, 128] float32; P = 128;
+ *   div the score divisor (sqrt(P) in the reference); out [B, Hkv, nb, top_k]
+ *   int32 (nb = ceil(T / 64) <= 1024, Hq / Hkv <= 8).
+ *   workspace: spruce_select_flat_workspace_bytes(B, Hkv, T, P) bytes, 16-byte
+ *   aligned (the projected block keys).
+ * spruce_select_flat_supported says whether a shape is covered (1) or not (0).
+ */
+int spruce_select_flat_supported(int64_t Hq, int64_t Hkv, int64_t T, int64_t D, int dtype, int64_t P);
+int64_t spruce_select_flat_workspace_bytes(int64_t B, int64_t Hkv, int64_t T, int64_t P);
+int spruce_select_flat(const void* q, const int64_t qs[4], const void* k, const int64_t ks[4], int64_t B,
+                       int64_t Hq, int64_t Hkv, int64_t T, int64_t D, int dtype, const float* wq,
+                       const float* wk, int64_t P, float div, int64_t top_k, void* workspace,
+                       int64_t workspace_bytes, int32_t* out, void* stream);
+
+/*
  * One parent level of the key-axis prototype tree.  Replaces
  * _merge_level_prototypes inside build_key_tree (selector/tree.py:79-145).
  *   child  [S, n, P, D] contiguous, S = layers * KV groups, dtype bf16/f16/f32.

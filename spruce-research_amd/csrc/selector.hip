@@ -1070,19 +1070,16 @@ __global__ __launch_bounds__(256) void causal_topk_kernel(const float* __restric
 // workgroup barriers.
 constexpr int kWaveTopkKb = 1024;
 constexpr int kWaveTopkPer = kWaveTopkKb / 64;
-__global__ __launch_bounds__(256) void causal_topk_wave_kernel(const float* __restrict__ scores, int64_t rows,
-                                                               int Qb, int Kb, int k, int32_t* __restrict__ out) {
+//
+// One wavefront selects the top k of srow[0..n) (n <= kWaveTopkKb) into o;
+// cw is 64 words of LDS private to the wavefront.  srow may be global or LDS.
+__device__ __forceinline__ void topk_row_wave(const float* __restrict__ srow, int n, int k, int32_t* __restrict__ o,
+                                              uint32_t* cw) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;  // whole wavefront; no block barrier follows
-  const int i = (int)(row % Qb);
-  const int n = i + 1 < Kb ? i + 1 : Kb;
-  int32_t* o = out + row * k;
   if (n <= k) {
     for (int t = lane; t < k; t += 64) o[t] = t < n ? t : -1;
     return;
   }
-  const float* srow = scores + row * Kb;
   uint32_t key[kWaveTopkPer];
 #pragma unroll
   for (int s = 0; s < kWaveTopkPer; ++s) {
@@ -1102,7 +1099,6 @@ __global__ __launch_bounds__(256) void causal_topk_wave_kernel(const float* __re
   // ends at the same T (the early exit is taken only at or above t0).
   // Otherwise the search runs over all 16 slots.
   uint32_t T = 0;
-  __shared__ uint32_t cands[4][64];
   int nc = kWaveTopkKb + 1;
   uint32_t t0 = 0;
   if (k <= 64) {
@@ -1118,7 +1114,6 @@ __global__ __launch_bounds__(256) void causal_topk_wave_kernel(const float* __re
     for (int s = 0; s < kWaveTopkPer; ++s) nc += __popcll(__ballot(key[s] >= t0));
   }
   if (nc <= 64) {
-    uint32_t* cw = cands[threadIdx.x >> 6];
     const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
     int base = 0;
 #pragma unroll
@@ -1166,6 +1161,442 @@ __global__ __launch_bounds__(256) void causal_topk_wave_kernel(const float* __re
     if (sel) o[out_base + __popcll(sb & lt)] = j;
     eq_base += __popcll(eqb);
     out_base += __popcll(sb);
+  }
+}
+
+__global__ __launch_bounds__(256) void causal_topk_wave_kernel(const float* __restrict__ scores, int64_t rows,
+                                                               int Qb, int Kb, int k, int32_t* __restrict__ out) {
+  __shared__ uint32_t cands[4][64];
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // whole wavefront; no block barrier follows
+  const int i = (int)(row % Qb);
+  const int n = i + 1 < Kb ? i + 1 : Kb;
+  topk_row_wave(scores + row * Kb, n, k, out + row * k, cands[threadIdx.x >> 6]);
+}
+
+
+// ---------------------------------------------------------------------------
+// Fused flat selector for the deployed shape: head_dim 128, projection dim
+// 128, 16-bit inputs, at most kPoolMaxG query heads per KV head and at most
+// kWaveTopkKb key blocks.  Two launches instead of four, with every value
+// produced by the operation sequences stated at the top of this file, so the
+// selected blocks are identical to those of the four-kernel route.
+//
+// Block pooling here gives each wavefront a whole 64-token block: lane =
+// 16 * lo + chunk (chunk = 8 dims, lo = 0..3), and the lane carries the four
+// token lanes l = lo + 4m (m = 0..3) of block_pool_fast_kernel at D = 128
+// (token t of a block in token lane t % 16, the 4 tokens of a token lane
+// folded in order), so every wavefront load reads 4 consecutive tokens x 256
+// contiguous bytes.  The halving tree over token lanes adds the same pairs:
+// st = 8 and 4 inside a lane (m + 2, then m + 1), st = 2 and 1 across lanes
+// (lane + 32, then lane + 16).
+constexpr int kFD = 128;                   // head_dim of the fused route
+constexpr int kFP = 128;                   // projection dim of the fused route
+constexpr int kFLanes = 16, kFPer = 4;     // pool_lanes(kFD / 8) and 64 / kFLanes
+constexpr int kFRows = 4;                  // query blocks per tile of the rows kernel
+static_assert(pool_lanes(kFD / 8) == kFLanes && kSelBlock / kFLanes == kFPer, "fused pooling shape");
+
+// Pins v in a register at this point: the sums of a token step are then
+// computed when the step is consumed, not sunk to their use after the
+// following steps' loads (which would keep every load's registers live).
+// An empty asm statement: no instruction is emitted.
+__device__ __forceinline__ void pin(float& v) { asm volatile("" : "+v"(v)); }
+
+// 16 bytes per lane from a buffer straight into LDS (buffer_load_dwordx4 ...
+// lds): lane l's bytes land at lds + 16 l.
+__device__ __forceinline__ void sel_load_lds16(__amdgpu_buffer_rsrc_t r, void* lds, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+}
+
+// Copies a [kFD][kFP] float32 weight matrix (64 KB) into LDS, 1 KB per
+// wavefront instruction, shared among nwaves wavefronts (wave = 0..nwaves-1).
+__device__ __forceinline__ void stage_weights(const float* w, float* lds, int wave, int nwaves) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(w), (short)0, kFD * kFP * 4, 0x00020000);
+  const int lane = threadIdx.x & 63;
+  for (int j = wave; j < kFD * kFP / 256; j += nwaves) sel_load_lds16(r, lds + 256 * j, 1024 * j + 16 * lane);
+}
+
+// Token of step (i, m) for lane group lo: token lane lo + 4m, i-th token of it.
+__device__ __forceinline__ int fused_token(int lo, int m, int i) { return lo + 4 * m + kFLanes * i; }
+
+// acc[m] holds token lane lo + 4m; leaves the block sum in lanes 0..15 (lo = 0).
+__device__ __forceinline__ void fused_tree_sum(float (&acc)[4][8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    acc[0][e] = acc[0][e] + acc[2][e];   // st = 8
+    acc[1][e] = acc[1][e] + acc[3][e];
+    acc[0][e] = acc[0][e] + acc[1][e];   // st = 4
+    acc[0][e] = acc[0][e] + __shfl_down(acc[0][e], 32);  // st = 2
+    acc[0][e] = acc[0][e] + __shfl_down(acc[0][e], 16);  // st = 1
+  }
+}
+
+__device__ __forceinline__ void fused_tree_max(float (&mx)[4][8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    mx[0][e] = max_total(mx[0][e], mx[2][e]);
+    mx[1][e] = max_total(mx[1][e], mx[3][e]);
+    mx[0][e] = max_total(mx[0][e], mx[1][e]);
+    mx[0][e] = max_total(mx[0][e], __shfl_down(mx[0][e], 32));
+    mx[0][e] = max_total(mx[0][e], __shfl_down(mx[0][e], 16));
+  }
+}
+
+struct SelKeysParams {
+  const void* k;
+  int64_t ks[4];
+  const float* wk;  // [kFD][kFP]
+  float* kp4;       // [BG][2][kFP / 4][nb][4]
+  int Hkv, T, nb, tiles;  // tiles = ceil(nb / kKeyBlocks) per (batch, KV head)
+};
+
+constexpr int kKeyBlocks = 8;  // key blocks per workgroup of select_keys_kernel, 2 per wavefront
+
+// Key side: one workgroup pools 8 key blocks of one (batch, KV head), two per
+// wavefront -- block mean and per-dim max -- and projects the 16 pooled rows
+// (fmaf chain over d from 0) with the weights staged in LDS, writing
+// kp4[bg][c][e / 4][j][e % 4] (c = 0 mean, 1 max).
+template <typename TIn>
+__global__ __launch_bounds__(256) void select_keys_kernel(const SelKeysParams p) {
+  __shared__ __attribute__((aligned(16))) float rows[2 * kKeyBlocks][kFD];  // row 2 * block + c
+  __shared__ __attribute__((aligned(16))) float wl[kFD][kFP];               // the key projection
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ch = lane & 15, lo = lane >> 4;
+  // (batch, KV head) fastest: the workgroups running together read all KV
+  // heads of the same tokens (rows that are adjacent in [B, T, H, D] storage).
+  const int BG = (int)(gridDim.x / p.tiles);
+  const int bg = blockIdx.x % BG;
+  const int j0 = (blockIdx.x / BG) * kKeyBlocks;
+  const int b = bg / p.Hkv, g = bg - (bg / p.Hkv) * p.Hkv;
+  const char* kb = static_cast<const char*>(p.k) +
+                   ((int64_t)b * p.ks[0] + (int64_t)g * p.ks[1] + 8 * ch) * TIn::bytes;
+  // All 32 loads of the wavefront's two blocks first (blocks and tokens
+  // clamped into the tensor so no load is conditional; tokens past T are
+  // replaced by zero when summed), then the weights into LDS.
+  Raw8<TIn> kr[2][kFPer][4];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    int blk = j0 + 2 * wave + u;
+    blk = blk < p.nb ? blk : p.nb - 1;
+#pragma unroll
+    for (int i = 0; i < kFPer; ++i)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int t = blk * kSelBlock + fused_token(lo, m, i);
+        kr[u][i][m] = raw8_at<TIn>(kb, (int64_t)(t < p.T ? t : p.T - 1) * p.ks[2]);
+      }
+  }
+  stage_weights(p.wk, &wl[0][0], wave, 4);
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int blk = j0 + 2 * wave + u;
+    if (blk >= p.nb) break;
+    const int t0 = blk * kSelBlock;
+    float acc[4][8], mx[4][8];
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mx[m][e] = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kFPer; ++i)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const bool valid = t0 + fused_token(lo, m, i) < p.T;
+        float s[8];
+        widen8<TIn>(kr[u][i][m], s);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          mx[m][e] = valid ? max_total(mx[m][e], s[e]) : mx[m][e];
+          s[e] = valid ? s[e] : 0.f;
+          acc[m][e] = (i == 0) ? s[e] : acc[m][e] + s[e];
+        }
+      }
+    fused_tree_sum(acc);
+    fused_tree_max(mx);
+    if (lane < 16) {
+      const int n = p.T - t0 < kSelBlock ? p.T - t0 : kSelBlock;
+      const float den = (float)n;
+      const int r = 2 * (2 * wave + u);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        rows[r][8 * ch + e] = acc[0][e] / den;
+        rows[r + 1][8 * ch + e] = mx[0][e];
+      }
+    }
+  }
+  __syncthreads();
+  // Projection: thread = output dim e, rows 8 * half .. 8 * half + 7.
+  const int e = tid & (kFP - 1), half = tid >> 7;
+  float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll 2
+  for (int d0 = 0; d0 < kFD; d0 += 4) {
+    const float w0 = wl[d0][e], w1 = wl[d0 + 1][e], w2 = wl[d0 + 2][e], w3 = wl[d0 + 3][e];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const float4 x = *reinterpret_cast<const float4*>(&rows[8 * half + r][d0]);
+      a[r] = __builtin_fmaf(x.x, w0, a[r]);
+      a[r] = __builtin_fmaf(x.y, w1, a[r]);
+      a[r] = __builtin_fmaf(x.z, w2, a[r]);
+      a[r] = __builtin_fmaf(x.w, w3, a[r]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const int row = 8 * half + r, j = j0 + (row >> 1), c = row & 1;
+    if (j < p.nb) p.kp4[((((int64_t)bg * 2 + c) * (kFP / 4) + (e >> 2)) * p.nb + j) * 4 + (e & 3)] = a[r];
+  }
+}
+
+struct SelRowsParams {
+  const void* q;
+  int64_t qs[4];
+  const float* wq;   // [kFD][kFP]
+  const float* kp4;  // select_keys_kernel's output
+  int32_t* out;      // [BG][nb][k]
+  int Hkv, T, nb, k, BG, row_tiles, ntiles;
+  int slice_bytes;  // bytes spanned by one (batch, KV group) slice of q
+  float div;
+};
+
+// Query side, persistent: workgroup w takes tiles w, w + grid, ... of kFRows
+// query blocks of one (batch, KV head), heaviest (latest) tiles first.  Waves
+// 0-3 pool the next tile's query blocks, one block each (G heads summed per
+// token, block mean; the same token-lane order as select_keys_kernel), while
+// waves 4-7 take the current tile through projection, MaxSim scores against
+// every causal key block and the wave top-k, all in LDS.  Each tile step has
+// two phases (scores | top-k) ending in a workgroup barrier; the pool waves
+// project their blocks themselves at the end of pooling.
+template <typename TIn, int G>
+__global__ __launch_bounds__(512) void select_rows_kernel(const SelRowsParams p) {
+  __shared__ __attribute__((aligned(16))) float qm[kFRows][kFD];      // pooled query block of each pool wave
+  __shared__ __attribute__((aligned(16))) float qp[2][kFRows][kFP];   // projected query blocks, double buffer
+  __shared__ __attribute__((aligned(16))) float sc[kFRows][kWaveTopkKb];
+  __shared__ __attribute__((aligned(16))) float wql[kFD][kFP];  // the query projection, staged once
+  __shared__ uint32_t cands[4][64];
+  // The wave index is taken through readfirstlane so that the pool / score
+  // split below is a scalar branch: each wave runs only its own side's
+  // barriers.
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grid = (int)gridDim.x;
+  const int mine = (p.ntiles - (int)blockIdx.x + grid - 1) / grid;  // tiles of this workgroup (>= 1)
+  auto tile_at = [&](int kk, int& bg, int& i0) __attribute__((always_inline)) {
+    const int tau = (int)blockIdx.x + kk * grid;
+    bg = tau % p.BG;
+    i0 = (p.row_tiles - 1 - tau / p.BG) * kFRows;
+  };
+
+  if (wave < 4) {
+    // ---- pool waves: wave w pools and projects block w of each tile (16
+    // steps (i, m) of G loads), token steps i = 0..2 | 3 in the two phases.  The
+    // ring holds the G loads of steps (i, m = 0..3); consuming step (i, m)
+    // issues step (i + 1, m), so up to 4G loads per lane stay in flight,
+    // across the phase barriers too (barriers do not wait for outstanding
+    // global loads).  Loads are issued without
+    // per-lane conditions (block and token clamped into the tensor; values
+    // past T are replaced by zero when consumed) so the compiler waits for
+    // each step's loads in issue order.
+    const int ch = lane & 15, lo = lane >> 4;
+    Raw8<TIn> ring[4][G];
+    float acc[4][8];
+    // Buffer loads from the (batch, KV group) slice: one 32-bit offset per
+    // lane and step, the head offset in an SGPR (the host checks that a slice
+    // spans less than 2^31 bytes).
+    const int hstride = (int)(p.qs[1] * 2);
+    auto issue = [&](int tk, int i, int m) __attribute__((always_inline)) {
+      tk = tk < mine ? tk : mine - 1;  // past the last tile: a repeated load, never consumed
+      int bg, i0;
+      tile_at(tk, bg, i0);
+      int blk = i0 + wave;
+      blk = blk < p.nb ? blk : p.nb - 1;
+      int t = blk * kSelBlock + fused_token(lo, m, i);
+      t = t < p.T ? t : p.T - 1;
+      const int b = bg / p.Hkv, g = bg - (bg / p.Hkv) * p.Hkv;
+      const char* base = static_cast<const char*>(p.q) + ((int64_t)b * p.qs[0] + (int64_t)(g * G) * p.qs[1]) * 2;
+      const __amdgpu_buffer_rsrc_t r =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, p.slice_bytes, 0x00020000);
+      const int voff = (int)(((int64_t)t * p.qs[2] + 8 * ch) * 2);
+#pragma unroll
+      for (int h = 0; h < G; ++h)
+        ring[m][h].a = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, h * hstride, 0));
+    };
+    auto consume = [&](int tk, int i) __attribute__((always_inline)) {
+      int bg, i0;
+      tile_at(tk, bg, i0);
+      const int blk = i0 + wave;
+      const bool live = blk < p.nb;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        float s[8];
+        widen8<TIn>(ring[m][0], s);
+#pragma unroll
+        for (int h = 1; h < G; ++h) {
+          float x[8];
+          widen8<TIn>(ring[m][h], x);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) s[e] = s[e] + x[e];
+        }
+        const bool valid = live && blk * kSelBlock + fused_token(lo, m, i) < p.T;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          s[e] = valid ? s[e] : 0.f;
+          acc[m][e] = (i == 0) ? s[e] : acc[m][e] + s[e];
+          pin(acc[m][e]);
+        }
+        // Slot m is consumed before its next loads are issued: the scheduler
+        // may not hoist them (that would hold two rings of registers).
+        __builtin_amdgcn_sched_barrier(0);
+        if (i + 1 < kFPer) issue(tk, i + 1, m);
+        else issue(tk + 1, 0, m);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    // The block mean goes through this wave's LDS row, then the wave projects
+    // it (outputs lane and lane + 64, fmaf chain over d from 0) into qp[buf].
+    auto finish = [&](int tk, int buf) __attribute__((always_inline)) {
+      int bg, i0;
+      tile_at(tk, bg, i0);
+      const int blk = i0 + wave;
+      if (blk >= p.nb) return;
+      fused_tree_sum(acc);
+      if (lane < 16) {
+        const int t0 = blk * kSelBlock;
+        const int n = p.T - t0 < kSelBlock ? p.T - t0 : kSelBlock;
+        const float den = (float)(G * n);
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = acc[0][e] / den;
+        float4* dst = reinterpret_cast<float4*>(&qm[wave][8 * ch]);
+        dst[0] = float4{o[0], o[1], o[2], o[3]};
+        dst[1] = float4{o[4], o[5], o[6], o[7]};
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      float a0 = 0.f, a1 = 0.f;
+#pragma unroll 4
+      for (int d0 = 0; d0 < kFD; d0 += 4) {
+        const float4 x = *reinterpret_cast<const float4*>(&qm[wave][d0]);
+        a0 = __builtin_fmaf(x.x, wql[d0][lane], a0);
+        a1 = __builtin_fmaf(x.x, wql[d0][64 + lane], a1);
+        a0 = __builtin_fmaf(x.y, wql[d0 + 1][lane], a0);
+        a1 = __builtin_fmaf(x.y, wql[d0 + 1][64 + lane], a1);
+        a0 = __builtin_fmaf(x.z, wql[d0 + 2][lane], a0);
+        a1 = __builtin_fmaf(x.z, wql[d0 + 2][64 + lane], a1);
+        a0 = __builtin_fmaf(x.w, wql[d0 + 3][lane], a0);
+        a1 = __builtin_fmaf(x.w, wql[d0 + 3][64 + lane], a1);
+      }
+      qp[buf][wave][lane] = a0;
+      qp[buf][wave][64 + lane] = a1;
+    };
+    // Tile steps -1 .. mine - 2 pool tile step + 1; the last step pools
+    // nothing.  Each tile's first token step is issued at the top of its
+    // iteration, so no load is in flight across the loop's back edge (loads
+    // carried there were copied between register sets after a full wait).
+#pragma unroll
+    for (int m = 0; m < 4; ++m) issue(0, 0, m);
+    for (int nxt = 0; nxt < mine; ++nxt) {
+      consume(nxt, 0);
+      consume(nxt, 1);
+      consume(nxt, 2);
+      __syncthreads();
+      consume(nxt, 3);
+      finish(nxt, nxt & 1);
+      __syncthreads();
+    }
+    __syncthreads();
+    __syncthreads();
+    return;
+  }
+
+  // ---- score waves
+  const int sw = wave - 4;
+  // The query projection into LDS, complete before the first barrier: the
+  // pool waves read it after that barrier (a barrier does not wait for
+  // another wave's loads).  s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15).
+  stage_weights(p.wq, &wql[0][0], sw, 4);
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  for (int kk = -1; kk < mine; ++kk) {
+    if (kk < 0) {
+      __syncthreads();
+      __syncthreads();
+      continue;
+    }
+    int bg, i0;
+    tile_at(kk, bg, i0);
+    const int buf = kk & 1;
+    // Phase 1: wave sw scores key blocks 256 sw .. 256 sw + 255 (4 per lane)
+    // against the tile's query blocks; keys past the last row's diagonal are
+    // not needed.
+    const int nk = i0 + kFRows < p.nb ? i0 + kFRows : p.nb;
+    const int jb = 256 * sw + 4 * lane;
+    if (256 * sw < nk) {
+      const float4* kp = reinterpret_cast<const float4*>(p.kp4) + (int64_t)bg * 2 * (kFP / 4) * p.nb;
+      float acc[kFRows][4][2];
+#pragma unroll
+      for (int r = 0; r < kFRows; ++r)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[r][u][0] = acc[r][u][1] = 0.f;
+      auto load_y = [&](int e4, float4 (&dst)[2][4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            dst[c][u] = kp[((int64_t)c * (kFP / 4) + e4) * p.nb + (jb + u < p.nb ? jb + u : p.nb - 1)];
+      };
+      auto step = [&](int e4, const float4 (&y)[2][4]) __attribute__((always_inline)) {
+        float4 x[kFRows];
+#pragma unroll
+        for (int r = 0; r < kFRows; ++r) x[r] = *reinterpret_cast<const float4*>(&qp[buf][r][4 * e4]);
+#pragma unroll
+        for (int r = 0; r < kFRows; ++r)
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+              float a = acc[r][u][c];
+              a = __builtin_fmaf(x[r].x, y[c][u].x, a);
+              a = __builtin_fmaf(x[r].y, y[c][u].y, a);
+              a = __builtin_fmaf(x[r].z, y[c][u].z, a);
+              a = __builtin_fmaf(x[r].w, y[c][u].w, a);
+              acc[r][u][c] = a;
+            }
+      };
+      // Ring of four register sets: the keys of dims 4(e4 + 4) load while
+      // those of dims 4 e4 are used (past the end a repeated load, unused).
+      float4 yb[4][2][4];
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) load_y(r4, yb[r4]);
+      for (int e4 = 0; e4 < kFP / 4; e4 += 4) {
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          step(e4 + r4, yb[r4]);
+          __builtin_amdgcn_sched_barrier(0);  // keep each set's reload right after its use
+          load_y(e4 + r4 + 4 < kFP / 4 ? e4 + r4 + 4 : kFP / 4 - 1, yb[r4]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < kFRows; ++r) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          float best = acc[r][u][0];
+          best = acc[r][u][1] > best ? acc[r][u][1] : best;
+          v[u] = best / p.div;
+        }
+        if (jb < nk) *reinterpret_cast<float4*>(&sc[r][jb]) = float4{v[0], v[1], v[2], v[3]};
+      }
+    }
+    __syncthreads();
+    // Phase 2: wave sw selects the top k of query block i0 + sw.
+    if (i0 + sw < p.nb) {
+      const int i = i0 + sw;
+      topk_row_wave(sc[sw], i + 1, p.k, p.out + ((int64_t)bg * p.nb + i) * p.k, cands[sw]);
+    }
+    __syncthreads();
   }
 }
 
@@ -1397,4 +1828,109 @@ extern "C" int spruce_causal_topk(const float* scores, int64_t R, int64_t Qb, in
   hipLaunchKernelGGL(causal_topk_kernel, dim3((unsigned)(R * Qb)), dim3(256), 0, (hipStream_t)stream, scores,
                      (int)Qb, (int)Kb, (int)k, out);
   return check_launch("causal_topk_kernel");
+}
+
+extern "C" int spruce_select_flat_supported(int64_t Hq, int64_t Hkv, int64_t T, int64_t D, int dtype, int64_t P) {
+  if (Hkv < 1 || Hq < Hkv || Hq % Hkv != 0 || T < 1) return 0;
+  const int64_t nb = (T + kSelBlock - 1) / kSelBlock;
+  return D == kFD && P == kFP && Hq / Hkv <= kPoolMaxG && nb <= kWaveTopkKb &&
+         (dtype == SPRUCE_DTYPE_BF16 || dtype == SPRUCE_DTYPE_F16);
+}
+
+extern "C" int64_t spruce_select_flat_workspace_bytes(int64_t B, int64_t Hkv, int64_t T, int64_t P) {
+  if (B < 1 || Hkv < 1 || T < 1 || P < 1) return -1;
+  return B * Hkv * 2 * P * ((T + kSelBlock - 1) / kSelBlock) * (int64_t)sizeof(float);
+}
+
+extern "C" int spruce_select_flat(const void* q, const int64_t qs[4], const void* k, const int64_t ks[4], int64_t B,
+                                  int64_t Hq, int64_t Hkv, int64_t T, int64_t D, int dtype, const float* wq,
+                                  const float* wk, int64_t P, float div, int64_t top_k, void* workspace,
+                                  int64_t workspace_bytes, int32_t* out, void* stream) {
+  SPRUCE_REQUIRE(q && qs && k && ks && wq && wk && out && workspace, "q, k, weights, workspace and out must be non-null");
+  SPRUCE_REQUIRE(B >= 1 && T >= 1 && Hkv >= 1 && Hq >= Hkv && Hq % Hkv == 0, "invalid shape");
+  SPRUCE_REQUIRE(B * Hkv < (1 << 20) && T < (1 << 30), "shape out of range");
+  SPRUCE_REQUIRE(spruce_select_flat_supported(Hq, Hkv, T, D, dtype, P),
+                 "fused selector needs head_dim %d, projection dim %d, a 16-bit dtype, at most %d query heads per KV "
+                 "head and at most %d key blocks (got D %lld, P %lld, dtype %d, G %lld, T %lld)",
+                 kFD, kFP, kPoolMaxG, kWaveTopkKb, (long long)D, (long long)P, dtype, (long long)(Hq / Hkv),
+                 (long long)T);
+  SPRUCE_REQUIRE(top_k >= 1 && top_k <= (1 << 20), "top_k must be >= 1, got %lld", (long long)top_k);
+  SPRUCE_REQUIRE(qs[3] == 1 && ks[3] == 1, "q and k need a contiguous last dim");
+  SPRUCE_REQUIRE(reinterpret_cast<uintptr_t>(q) % 16 == 0 && qs[0] % 8 == 0 && qs[1] % 8 == 0 && qs[2] % 8 == 0 &&
+                     reinterpret_cast<uintptr_t>(k) % 16 == 0 && ks[0] % 8 == 0 && ks[1] % 8 == 0 && ks[2] % 8 == 0,
+                 "q and k rows must be 16-byte aligned");
+  SPRUCE_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0, "workspace must be 16-byte aligned");
+  const int64_t need = spruce_select_flat_workspace_bytes(B, Hkv, T, P);
+  SPRUCE_REQUIRE(workspace_bytes >= need, "workspace too small: %lld bytes, need %lld", (long long)workspace_bytes,
+                 (long long)need);
+  const int nb = (int)((T + kSelBlock - 1) / kSelBlock);
+  const int BG = (int)(B * Hkv);
+  SelKeysParams kp{};
+  kp.k = k;
+  for (int i = 0; i < 4; ++i) kp.ks[i] = ks[i];
+  kp.wk = wk;
+  kp.kp4 = static_cast<float*>(workspace);
+  kp.Hkv = (int)Hkv;
+  kp.T = (int)T;
+  kp.nb = nb;
+  kp.tiles = (nb + kKeyBlocks - 1) / kKeyBlocks;
+  const int64_t kgrid = (int64_t)BG * kp.tiles;
+  SPRUCE_REQUIRE(kgrid < ((int64_t)1 << 31), "grid too large");
+  if (dtype == SPRUCE_DTYPE_BF16)
+    hipLaunchKernelGGL(select_keys_kernel<InBF16>, dim3((unsigned)kgrid), dim3(256), 0, (hipStream_t)stream, kp);
+  else
+    hipLaunchKernelGGL(select_keys_kernel<InF16>, dim3((unsigned)kgrid), dim3(256), 0, (hipStream_t)stream, kp);
+  int rc = check_launch("select_keys_kernel");
+  if (rc != SPRUCE_OK) return rc;
+
+  SelRowsParams rp{};
+  rp.q = q;
+  for (int i = 0; i < 4; ++i) rp.qs[i] = qs[i];
+  rp.wq = wq;
+  rp.kp4 = static_cast<const float*>(workspace);
+  rp.out = out;
+  rp.Hkv = (int)Hkv;
+  rp.T = (int)T;
+  rp.nb = nb;
+  rp.k = (int)top_k;
+  rp.BG = BG;
+  rp.row_tiles = (nb + kFRows - 1) / kFRows;
+  const int64_t ntiles = (int64_t)BG * rp.row_tiles;
+  SPRUCE_REQUIRE(ntiles < ((int64_t)1 << 30), "too many row tiles");
+  rp.ntiles = (int)ntiles;
+  rp.div = div;
+  const int64_t G = Hq / Hkv;
+  const int64_t slice = ((T - 1) * qs[2] + (G - 1) * qs[1] + D) * 2;
+  SPRUCE_REQUIRE(qs[1] >= 0 && qs[2] >= 0 && slice < ((int64_t)1 << 31) && (G - 1) * qs[1] * 2 < ((int64_t)1 << 31),
+                 "fused selector needs each (batch, KV group) slice of q within 2^31 bytes (got %lld)",
+                 (long long)slice);
+  rp.slice_bytes = (int)slice;
+  // One persistent workgroup per CU (each holds 8 waves), at most one per tile.
+  int dev = 0, cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return set_error((int)e, "device query failed: %s", hipGetErrorString(e));
+  const int grid = (int)(ntiles < cus ? ntiles : cus);
+  const bool bf = dtype == SPRUCE_DTYPE_BF16;
+  const dim3 g3((unsigned)grid), b3(512);
+  hipStream_t st = (hipStream_t)stream;
+  switch (Hq / Hkv) {
+#define SPRUCE_ROWS_CASE(GG)                                                                            \
+  case GG:                                                                                              \
+    if (bf) hipLaunchKernelGGL((select_rows_kernel<InBF16, GG>), g3, b3, 0, st, rp);                    \
+    else hipLaunchKernelGGL((select_rows_kernel<InF16, GG>), g3, b3, 0, st, rp);                        \
+    break;
+    SPRUCE_ROWS_CASE(1)
+    SPRUCE_ROWS_CASE(2)
+    SPRUCE_ROWS_CASE(3)
+    SPRUCE_ROWS_CASE(4)
+    SPRUCE_ROWS_CASE(5)
+    SPRUCE_ROWS_CASE(6)
+    SPRUCE_ROWS_CASE(7)
+    SPRUCE_ROWS_CASE(8)
+#undef SPRUCE_ROWS_CASE
+    default:
+      return set_error(SPRUCE_EINVAL, "unsupported query heads per KV head: %lld", (long long)(Hq / Hkv));
+  }
+  return check_launch("select_rows_kernel");
 }

@@ -55,6 +55,10 @@ _SIGNATURES = {
                                    _p, ctypes.c_int, _p],
     "spruce_gate_scores": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int, _p, _p],
     "spruce_causal_topk": [_p, _i64, _i64, _i64, _i64, _p, _p],
+    "spruce_select_flat_supported": [_i64, _i64, _i64, _i64, ctypes.c_int, _i64],
+    "spruce_select_flat": [
+        _p, _STRIDES, _p, _STRIDES, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _p, _i64, ctypes.c_float,
+        _i64, _p, _i64, _p, _p],
     "spruce_teacher_block_mass": [
         _p, _STRIDES, _p, _STRIDES, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int,
         _p, _p, ctypes.c_size_t, _p],
@@ -132,6 +136,8 @@ def lib():
         handle.spruce_teacher_schedule_workspace_bytes.argtypes = [_i64, _i64, _i64, ctypes.c_int]
         handle.spruce_kv_summary_workspace_bytes.restype = ctypes.c_size_t
         handle.spruce_kv_summary_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64]
+        handle.spruce_select_flat_workspace_bytes.restype = _i64
+        handle.spruce_select_flat_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64]
         _lib = handle
     return _lib
 

@@ -200,3 +200,30 @@ def test_summary_table_dtype_validation_before_launch():
     for dtype, sum_dtype in ((0, 1), (1, 0), (2, 0), (0, 7)):
         assert call(dtype, sum_dtype) == -1, (dtype, sum_dtype)
         assert "float32 or the 16-bit input dtype" in spruce_hip.last_error(), spruce_hip.last_error()
+
+
+def test_fused_selector_support_and_validation_before_launch():
+    lib = spruce_hip.lib()
+    bf16, f32 = 0, 2
+    assert lib.spruce_select_flat_supported(28, 4, 65536, 128, bf16, 128) == 1
+    assert lib.spruce_select_flat_supported(28, 4, 65537, 128, bf16, 128) == 0     # 1025 key blocks
+    assert lib.spruce_select_flat_supported(36, 4, 1000, 128, bf16, 128) == 0      # 9 query heads per KV head
+    assert lib.spruce_select_flat_supported(28, 4, 1000, 64, bf16, 128) == 0
+    assert lib.spruce_select_flat_supported(28, 4, 1000, 128, f32, 128) == 0
+    assert lib.spruce_select_flat_supported(28, 4, 1000, 128, bf16, 64) == 0
+    assert lib.spruce_select_flat_workspace_bytes(1, 4, 65536, 128) == 4 * 2 * 128 * 1024 * 4
+    fake = ctypes.c_void_p(1 << 20)
+    qs, ks = _strides(0, 128 * 1000, 128, 1), _strides(0, 128 * 1000, 128, 1)
+    need = lib.spruce_select_flat_workspace_bytes(1, 4, 1000, 128)
+
+    def call(Hq=28, T=1000, D=128, dtype=bf16, P=128, top_k=32, ws_bytes=need, ws=fake, qs=qs, out=fake):
+        return lib.spruce_select_flat(fake, qs, fake, ks, 1, Hq, 4, T, D, dtype, fake, fake, P, 11.3, top_k,
+                                      ws, ws_bytes, out, None)
+    cases = [(dict(D=64), "head_dim 128"), (dict(dtype=f32), "head_dim 128"), (dict(Hq=36), "head_dim 128"),
+             (dict(T=65537), "head_dim 128"), (dict(P=64), "head_dim 128"), (dict(top_k=0), "top_k"),
+             (dict(ws_bytes=need - 4), "workspace too small"), (dict(ws=ctypes.c_void_p((1 << 20) + 4)), "aligned"),
+             (dict(qs=_strides(0, 128 * 1000, 100, 1)), "16-byte aligned"), (dict(out=None), "non-null"),
+             (dict(Hq=30), "invalid shape")]
+    for kwargs, message in cases:
+        assert call(**kwargs) == -1, kwargs
+        assert message in spruce_hip.last_error(), (kwargs, spruce_hip.last_error())

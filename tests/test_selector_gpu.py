@@ -302,3 +302,65 @@ def test_cfg3_full_size_selected_blocks_bit_exact():
     fast = select_blocks(q.transpose(1, 2).contiguous().to(DEV).transpose(1, 2), k.to(DEV),
                          Wq.to(DEV), Wk.to(DEV), top_k=32)
     assert np.array_equal(_np(fast), exp["selected"])
+    # The two-launch fused route at full size.
+    from selector.select import select_blocks_fused
+    fused = select_blocks_fused(q.transpose(1, 2).contiguous().to(DEV).transpose(1, 2), k.to(DEV),
+                                Wq.to(DEV), Wk.to(DEV), top_k=32)
+    assert np.array_equal(_np(fused), exp["selected"])
+
+
+# The fused route (key side in one launch, one persistent launch that pools
+# and projects the next tile of query blocks while the current one is scored
+# and selected) against the four-launch route and the oracle.  Cases: every query
+# heads per KV head from 1 to 8, ragged T (partial last block, partial last
+# tile of 4 blocks), B > 1, both 16-bit dtypes, strided [B, T, H, D] storage,
+# k = 1, k above 64 (the top-k's full search) and k above the block count, and
+# the 1024-block maximum.
+@pytest.mark.parametrize("B,Hq,Hkv,T,k,dtype,bthd", [
+    (2, 8, 2, 1000, 32, torch.bfloat16, True),
+    (1, 7, 1, 64, 8, torch.float16, False),
+    (1, 8, 1, 5000, 64, torch.bfloat16, True),
+    (3, 3, 3, 777, 5, torch.float16, False),
+    (1, 10, 2, 4113, 33, torch.bfloat16, False),
+    (1, 6, 2, 65536, 100, torch.bfloat16, True),
+    (1, 2, 1, 130, 200, torch.float16, True),
+    (2, 12, 2, 3000, 1, torch.bfloat16, True),
+    (1, 14, 2, 1601, 16, torch.float16, True),
+])
+def test_fused_route_equals_four_launch_route(B, Hq, Hkv, T, k, dtype, bthd):
+    from selector.select import fused_route_applies, select_blocks_fused
+    D = P = 128
+    print(f"fused selector B={B} Hq={Hq} Hkv={Hkv} T={T} k={k} {dtype}", flush=True)
+    gen = torch.Generator().manual_seed(T + Hq + k)
+    if bthd:
+        q = torch.randn(B, T, Hq, D, generator=gen).to(dtype).to(DEV).transpose(1, 2)
+    else:
+        q = torch.randn(B, Hq, T, D, generator=gen).to(dtype).to(DEV)
+    kk = torch.randn(B, Hkv, T, D, generator=gen).to(dtype).to(DEV)
+    Wq = (torch.randn(D, P, generator=gen) / D ** 0.5).to(DEV)
+    Wk = (torch.randn(D, P, generator=gen) / D ** 0.5).to(DEV)
+    assert fused_route_applies(q, kk, Wq, Wk)
+    fused = select_blocks_fused(q, kk, Wq, Wk, top_k=k)
+    four = select_blocks(q, kk, Wq, Wk, top_k=k, return_intermediates=True)["selected"]
+    torch.cuda.synchronize()
+    assert fused.shape == four.shape == (B, 1, Hkv, (T + 63) // 64, k)
+    assert torch.equal(fused, four)
+    assert torch.equal(select_blocks(q, kk, Wq, Wk, top_k=k), fused)   # the default (four-launch) route
+    if T <= 5000:
+        exp = osel.flat_select(q.float().cpu().numpy(), kk.float().cpu().numpy(), Wq.cpu().numpy(),
+                               Wk.cpu().numpy(), top_k=k)
+        assert np.array_equal(_np(fused), exp["selected"])
+
+
+def test_fused_route_applies_only_to_its_shapes():
+    from selector.select import fused_route_applies
+    W = torch.zeros(128, 128, device=DEV)
+    q = torch.zeros(1, 8, 256, 128, device=DEV, dtype=torch.bfloat16)
+    k = torch.zeros(1, 2, 256, 128, device=DEV, dtype=torch.bfloat16)
+    assert fused_route_applies(q, k, W, W)
+    assert not fused_route_applies(q.float(), k.float(), W, W)                        # float32 inputs
+    assert not fused_route_applies(q[..., :64], k[..., :64], W[:64], W[:64])          # head_dim 64
+    assert not fused_route_applies(q, k, W[:, :64], W[:, :64])                         # projection dim 64
+    assert not fused_route_applies(torch.zeros(1, 18, 256, 128, device=DEV, dtype=torch.bfloat16), k, W, W)  # G 9
+    long_q = torch.zeros(1, 2, 1024 * 64 + 1, 128, device=DEV, dtype=torch.bfloat16)   # 1025 key blocks
+    assert not fused_route_applies(long_q, long_q[:, :1], W, W)
