@@ -1404,7 +1404,6 @@ __global__ __launch_bounds__(512) void select_rows_kernel(const SelRowsParams p)
     // Buffer loads from the (batch, KV group) slice: one 32-bit offset per
     // lane and step, the head offset in an SGPR (the host checks that a slice
     // spans less than 2^31 bytes).
-    const int hstride = (int)(p.qs[1] * 2);
     auto issue = [&](int tk, int i, int m) __attribute__((always_inline)) {
       tk = tk < mine ? tk : mine - 1;  // past the last tile: a repeated load, never consumed
       int bg, i0;
@@ -1420,7 +1419,8 @@ __global__ __launch_bounds__(512) void select_rows_kernel(const SelRowsParams p)
       const int voff = (int)(((int64_t)t * p.qs[2] + 8 * ch) * 2);
 #pragma unroll
       for (int h = 0; h < G; ++h)
-        ring[m][h].a = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, h * hstride, 0));
+        ring[m][h].a = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, (int)((int64_t)h * p.qs[1] * 2), 0));
     };
     auto consume = [&](int tk, int i) __attribute__((always_inline)) {
       int bg, i0;
