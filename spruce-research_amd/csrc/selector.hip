@@ -1326,6 +1326,10 @@ __global__ __launch_bounds__(256) void select_keys_kernel(const SelKeysParams p)
       }
     }
   }
+  // Every wave's share of the weights is in LDS before the barrier.  The
+  // barrier's release fence already waits for this wave's loads into LDS; the
+  // explicit s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15) states it.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
   __syncthreads();
   // Projection: thread = output dim e, rows 8 * half .. 8 * half + 7.
   const int e = tid & (kFP - 1), half = tid >> 7;
@@ -1514,8 +1518,9 @@ __global__ __launch_bounds__(512) void select_rows_kernel(const SelRowsParams p)
   // ---- score waves
   const int sw = wave - 4;
   // The query projection into LDS, complete before the first barrier: the
-  // pool waves read it after that barrier (a barrier does not wait for
-  // another wave's loads).  s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15).
+  // pool waves read it after that barrier.  The barrier's release fence
+  // already waits for this wave's loads into LDS; the explicit s_waitcnt
+  // vmcnt(0) expcnt(7) lgkmcnt(15) states it.
   stage_weights(p.wq, &wql[0][0], sw, 4);
   __builtin_amdgcn_s_waitcnt(0x0F70);
   for (int kk = -1; kk < mine; ++kk) {
