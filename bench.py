@@ -450,7 +450,7 @@ def main():
             "gbps": round(by3 / (m3 * 1e-3) / 1e9, 1),
             "frac_hbm_peak": round(by3 / (m3 * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
             "compulsory_bytes": by3, "top_k": 32,
-            "stages": "pool (Q group+block mean, K mean/max) -> project -> MaxSim scores -> causal top-k",
+            "stages": "pool (Q group+block mean, K mean/max) and project, one launch -> MaxSim scores -> causal top-k",
         }
         if not args.no_cpu:
             configs["cfg3_selector_64k"]["cpu_baseline"] = cpu_baseline_selector(

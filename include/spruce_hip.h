@@ -343,6 +343,23 @@ int spruce_causal_topk(const float* scores, int64_t R, int64_t Qb, int64_t Kb, i
                        void* stream);
 
 /*
+ * Block pooling and the gate projection in one launch: the values of
+ * spruce_selector_pool (query group-and-block mean, key block mean and max;
+ * teacher/chunked_extract.py:27-80 and :75-80 with the builder's max summary)
+ * followed by spruce_gate_project2 (selector/gate.py:120-127), without the
+ * pooled summaries in memory.
+ *   q [B, Hq, T, 128], k [B, Hkv, T, 128] (any strides, contiguous last dim,
+ *   16-byte aligned rows, each (batch, KV group) slice within 2^31 bytes),
+ *   bf16 or f16, Hq / Hkv <= 8; wq, wk [128, 128] float32; P = 128.
+ *   qp [B, Hkv, nb, 128] and kp [B, Hkv, nb, 2, 128] float32 (nb = ceil(T / 64);
+ *   kp's [.., 0, :] is the projected block mean, [.., 1, :] the projected max).
+ */
+int spruce_selector_pool_project(const void* q, const int64_t qs[4], const void* k, const int64_t ks[4],
+                                 int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D, int dtype,
+                                 const float* wq, const float* wk, int64_t P, float* qp, float* kp,
+                                 void* stream);
+
+/*
  * The whole flat selector in two launches: the reference's flat route
  * (scripts/eval_gate.py:70-72) -- pooled block features
  * (teacher/chunked_extract.py:27-80), FlatGate MaxSim scoring

@@ -1353,6 +1353,174 @@ __global__ __launch_bounds__(256) void select_keys_kernel(const SelKeysParams p)
   }
 }
 
+// ---------------------------------------------------------------------------
+// Pooling and projection of the selector's query and key blocks in one
+// persistent launch (head_dim = projection dim = 128, 16-bit inputs, G <= 8):
+// the values of spruce_selector_pool followed by spruce_gate_project2, without
+// the pooled summaries' round trip through HBM or the projection launch.
+// Every wavefront takes (batch, KV head, block) tasks on its own (no
+// workgroup barrier after the weights are staged): it pools the query block
+// (G heads summed per token, block mean) and the key block (mean and per-dim
+// max) with the token-lane order and trees of select_keys_kernel, then
+// projects the three rows (fmaf chains over d from 0) with both weight
+// matrices in LDS.  A two-slot ring holds the G query loads and the key load
+// of a token step; consuming step s issues step s + 2, so 2(G + 1) loads per
+// lane stay in flight, 8 wavefronts per CU.
+struct PoolProjParams {
+  const void* q;
+  const void* k;
+  int64_t qs[4], ks[4];
+  const float* wq;  // [kFD][kFP]
+  const float* wk;  // [kFD][kFP]
+  float* qp;        // [BG][nb][kFP]
+  float* kp;        // [BG][nb][2][kFP]
+  int Hkv, T, nb, BG, ntasks;
+  int qslice, kslice;  // bytes spanned by one (batch, KV group) slice of q / k
+};
+
+template <typename TIn, int G>
+__global__ __launch_bounds__(512) void pool_project_kernel(const PoolProjParams p) {
+  __shared__ __attribute__((aligned(16))) float wql[kFD][kFP];
+  __shared__ __attribute__((aligned(16))) float wkl[kFD][kFP];
+  __shared__ __attribute__((aligned(16))) float rowbuf[8][3][kFD];  // per wave: q mean, k mean, k max
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ch = lane & 15, lo = lane >> 4;
+  stage_weights(p.wq, &wql[0][0], wave, 8);
+  stage_weights(p.wk, &wkl[0][0], wave, 8);
+  // The barrier's release fence waits for this wave's loads into LDS; the
+  // explicit s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15) states it.
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __syncthreads();
+  const int nw = (int)gridDim.x * 8;
+  const int w0 = (int)blockIdx.x * 8 + wave;
+  const int mine = (p.ntasks - w0 + nw - 1) / nw;  // tasks w0, w0 + nw, ... (0 when w0 >= ntasks)
+  if (mine <= 0) return;
+  Raw8<TIn> qr[2][G], kr[2];
+  float aq[4][8], ak[4][8], mk[4][8];
+  auto task_of = [&](int n, int& bg, int& blk) __attribute__((always_inline)) {
+    const int tau = w0 + n * nw;
+    bg = tau % p.BG;  // (batch, KV head) fastest: the waves running together read neighbouring rows
+    blk = tau / p.BG;
+  };
+  auto issue = [&](int n, int st) __attribute__((always_inline)) {
+    n = n < mine ? n : mine - 1;  // past the last task: a repeated load, never consumed
+    int bg, blk;
+    task_of(n, bg, blk);
+    const int i = st >> 2, m = st & 3;
+    int t = blk * kSelBlock + fused_token(lo, m, i);
+    t = t < p.T ? t : p.T - 1;
+    const int b = bg / p.Hkv, g = bg - (bg / p.Hkv) * p.Hkv;
+    const char* qb = static_cast<const char*>(p.q) + ((int64_t)b * p.qs[0] + (int64_t)(g * G) * p.qs[1]) * 2;
+    const char* kb = static_cast<const char*>(p.k) + ((int64_t)b * p.ks[0] + (int64_t)g * p.ks[1]) * 2;
+    const __amdgpu_buffer_rsrc_t rq =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(qb), (short)0, p.qslice, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(kb), (short)0, p.kslice, 0x00020000);
+    const int qoff = (int)(((int64_t)t * p.qs[2] + 8 * ch) * 2);
+    const int koff = (int)(((int64_t)t * p.ks[2] + 8 * ch) * 2);
+    const int sl = st & 1;
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+      qr[sl][h].a = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, qoff, (int)((int64_t)h * p.qs[1] * 2), 0));
+    kr[sl].a = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, koff, 0, 0));
+  };
+  auto consume = [&](int n, int st) __attribute__((always_inline)) {
+    int bg, blk;
+    task_of(n, bg, blk);
+    const int i = st >> 2, m = st & 3, sl = st & 1;
+    const bool valid = blk * kSelBlock + fused_token(lo, m, i) < p.T;
+    float s[8], x[8];
+    widen8<TIn>(qr[sl][0], s);
+#pragma unroll
+    for (int h = 1; h < G; ++h) {
+      widen8<TIn>(qr[sl][h], x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s[e] = s[e] + x[e];
+    }
+    widen8<TIn>(kr[sl], x);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      s[e] = valid ? s[e] : 0.f;
+      aq[m][e] = (i == 0) ? s[e] : aq[m][e] + s[e];
+      const float mprev = (i == 0) ? -INFINITY : mk[m][e];
+      mk[m][e] = valid ? max_total(mprev, x[e]) : mprev;
+      x[e] = valid ? x[e] : 0.f;
+      ak[m][e] = (i == 0) ? x[e] : ak[m][e] + x[e];
+      pin(aq[m][e]);
+      pin(ak[m][e]);
+      pin(mk[m][e]);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // slot sl is consumed before its next loads are issued
+    if (st + 2 < 16) issue(n, st + 2);
+    else issue(n + 1, st + 2 - 16);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto finish = [&](int n) __attribute__((always_inline)) {
+    int bg, blk;
+    task_of(n, bg, blk);
+    fused_tree_sum(aq);
+    fused_tree_sum(ak);
+    fused_tree_max(mk);
+    if (lane < 16) {
+      const int t0 = blk * kSelBlock;
+      const int cnt = p.T - t0 < kSelBlock ? p.T - t0 : kSelBlock;
+      const float dq = (float)(G * cnt), dk = (float)cnt;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        rowbuf[wave][0][8 * ch + e] = aq[0][e] / dq;
+        rowbuf[wave][1][8 * ch + e] = ak[0][e] / dk;
+        rowbuf[wave][2][8 * ch + e] = mk[0][e];
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float a[3][2] = {{0.f, 0.f}, {0.f, 0.f}, {0.f, 0.f}};
+#pragma unroll 2
+    for (int d0 = 0; d0 < kFD; d0 += 4) {
+      float4 xr[3];
+#pragma unroll
+      for (int r = 0; r < 3; ++r) xr[r] = *reinterpret_cast<const float4*>(&rowbuf[wave][r][d0]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float wq0 = wql[d0 + u][lane], wq1 = wql[d0 + u][64 + lane];
+        const float wk0 = wkl[d0 + u][lane], wk1 = wkl[d0 + u][64 + lane];
+        const float xq = u == 0 ? xr[0].x : u == 1 ? xr[0].y : u == 2 ? xr[0].z : xr[0].w;
+        const float xm = u == 0 ? xr[1].x : u == 1 ? xr[1].y : u == 2 ? xr[1].z : xr[1].w;
+        const float xx = u == 0 ? xr[2].x : u == 1 ? xr[2].y : u == 2 ? xr[2].z : xr[2].w;
+        a[0][0] = __builtin_fmaf(xq, wq0, a[0][0]);
+        a[0][1] = __builtin_fmaf(xq, wq1, a[0][1]);
+        a[1][0] = __builtin_fmaf(xm, wk0, a[1][0]);
+        a[1][1] = __builtin_fmaf(xm, wk1, a[1][1]);
+        a[2][0] = __builtin_fmaf(xx, wk0, a[2][0]);
+        a[2][1] = __builtin_fmaf(xx, wk1, a[2][1]);
+      }
+    }
+    float* oq = p.qp + ((int64_t)bg * p.nb + blk) * kFP;
+    float* ok = p.kp + ((int64_t)bg * p.nb + blk) * 2 * kFP;
+    oq[lane] = a[0][0];
+    oq[64 + lane] = a[0][1];
+    ok[lane] = a[1][0];
+    ok[64 + lane] = a[1][1];
+    ok[kFP + lane] = a[2][0];
+    ok[kFP + 64 + lane] = a[2][1];
+    // The row buffer is rewritten by the next task's tree only after every
+    // lane has read it here.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  issue(0, 0);
+  issue(0, 1);
+  for (int n = 0; n < mine; ++n) {
+#pragma unroll
+    for (int st = 0; st < 16; ++st) consume(n, st);
+    finish(n);
+  }
+}
+
 struct SelRowsParams {
   const void* q;
   int64_t qs[4];
@@ -1938,4 +2106,77 @@ extern "C" int spruce_select_flat(const void* q, const int64_t qs[4], const void
       return set_error(SPRUCE_EINVAL, "unsupported query heads per KV head: %lld", (long long)(Hq / Hkv));
   }
   return check_launch("select_rows_kernel");
+}
+
+extern "C" int spruce_selector_pool_project(const void* q, const int64_t qs[4], const void* k, const int64_t ks[4],
+                                            int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D, int dtype,
+                                            const float* wq, const float* wk, int64_t P, float* qp, float* kp,
+                                            void* stream) {
+  SPRUCE_REQUIRE(q && qs && k && ks && wq && wk && qp && kp, "q, k, weights and outputs must be non-null");
+  SPRUCE_REQUIRE(B >= 1 && T >= 1 && Hkv >= 1 && Hq >= Hkv && Hq % Hkv == 0, "invalid shape");
+  SPRUCE_REQUIRE(D == kFD && P == kFP && Hq / Hkv <= kPoolMaxG &&
+                     (dtype == SPRUCE_DTYPE_BF16 || dtype == SPRUCE_DTYPE_F16),
+                 "pooled projection needs head_dim %d, projection dim %d, a 16-bit dtype and at most %d query "
+                 "heads per KV head (got D %lld, P %lld, dtype %d, G %lld)",
+                 kFD, kFP, kPoolMaxG, (long long)D, (long long)P, dtype, (long long)(Hq / Hkv));
+  SPRUCE_REQUIRE(qs[3] == 1 && ks[3] == 1, "q and k need a contiguous last dim");
+  SPRUCE_REQUIRE(reinterpret_cast<uintptr_t>(q) % 16 == 0 && qs[0] % 8 == 0 && qs[1] % 8 == 0 && qs[2] % 8 == 0 &&
+                     reinterpret_cast<uintptr_t>(k) % 16 == 0 && ks[0] % 8 == 0 && ks[1] % 8 == 0 && ks[2] % 8 == 0,
+                 "q and k rows must be 16-byte aligned");
+  const int64_t G = Hq / Hkv;
+  const int64_t qslice = ((T - 1) * qs[2] + (G - 1) * qs[1] + D) * 2;
+  const int64_t kslice = ((T - 1) * ks[2] + D) * 2;
+  SPRUCE_REQUIRE(qs[1] >= 0 && qs[2] >= 0 && ks[2] >= 0 && qslice < ((int64_t)1 << 31) &&
+                     kslice < ((int64_t)1 << 31),
+                 "pooled projection needs each (batch, KV group) slice of q and k within 2^31 bytes");
+  const int64_t nb = (T + kSelBlock - 1) / kSelBlock;
+  const int64_t ntasks = B * Hkv * nb;
+  SPRUCE_REQUIRE(ntasks < ((int64_t)1 << 30), "too many blocks");
+  PoolProjParams pp{};
+  pp.q = q;
+  pp.k = k;
+  for (int i = 0; i < 4; ++i) {
+    pp.qs[i] = qs[i];
+    pp.ks[i] = ks[i];
+  }
+  pp.wq = wq;
+  pp.wk = wk;
+  pp.qp = qp;
+  pp.kp = kp;
+  pp.Hkv = (int)Hkv;
+  pp.T = (int)T;
+  pp.nb = (int)nb;
+  pp.BG = (int)(B * Hkv);
+  pp.ntasks = (int)ntasks;
+  pp.qslice = (int)qslice;
+  pp.kslice = (int)kslice;
+  // One persistent workgroup of 8 wavefronts per CU (the weights fill 128 KB of LDS).
+  int dev = 0, cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return set_error((int)e, "device query failed: %s", hipGetErrorString(e));
+  const int64_t need = (ntasks + 7) / 8;
+  const int grid = (int)(need < cus ? need : cus);
+  const bool bf = dtype == SPRUCE_DTYPE_BF16;
+  const dim3 g3((unsigned)grid), b3(512);
+  hipStream_t st = (hipStream_t)stream;
+  switch (G) {
+#define SPRUCE_PP_CASE(GG)                                                                \
+  case GG:                                                                                \
+    if (bf) hipLaunchKernelGGL((pool_project_kernel<InBF16, GG>), g3, b3, 0, st, pp);     \
+    else hipLaunchKernelGGL((pool_project_kernel<InF16, GG>), g3, b3, 0, st, pp);         \
+    break;
+    SPRUCE_PP_CASE(1)
+    SPRUCE_PP_CASE(2)
+    SPRUCE_PP_CASE(3)
+    SPRUCE_PP_CASE(4)
+    SPRUCE_PP_CASE(5)
+    SPRUCE_PP_CASE(6)
+    SPRUCE_PP_CASE(7)
+    SPRUCE_PP_CASE(8)
+#undef SPRUCE_PP_CASE
+    default:
+      return set_error(SPRUCE_EINVAL, "unsupported query heads per KV head: %lld", (long long)G);
+  }
+  return check_launch("pool_project_kernel");
 }

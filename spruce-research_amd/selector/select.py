@@ -65,6 +65,57 @@ def pool_blocks(query=None, key=None):
     return q_mean, k_sum
 
 
+def pool_project_applies(query, key, Wq, Wk):
+    """True when ``pool_project`` covers the shapes: head_dim and projection
+    dim 128 (one ``[128, 128]`` float32 weight per side), bf16 or fp16 query
+    and key of one dtype, at most 8 query heads per KV head, each (batch, KV
+    group) slice of q and k within 2^31 bytes."""
+    if query is None or key is None or query.dim() != 4 or key.dim() != 4:
+        return False
+    if Wq.dim() != 2 or Wq.shape != (128, 128) or Wk.shape != (128, 128):
+        return False
+    if Wq.dtype != torch.float32 or Wk.dtype != torch.float32:
+        return False
+    if query.dtype != key.dtype or query.dtype not in (torch.bfloat16, torch.float16):
+        return False
+    B, Hq, T, D = query.shape
+    Hkv = key.shape[1]
+    if D != 128 or key.shape[0] != B or key.shape[2:] != query.shape[2:] or Hq % Hkv or Hq // Hkv > 8:
+        return False
+    qs, ks = query.stride(), key.stride()
+    if qs[3] != 1 or ks[3] != 1 or min(qs[1], qs[2], ks[2]) < 0:
+        return False
+    G = Hq // Hkv
+    return ((T - 1) * qs[2] + (G - 1) * qs[1] + D) * 2 < 2 ** 31 and ((T - 1) * ks[2] + D) * 2 < 2 ** 31
+
+
+def pool_project(query, key, Wq, Wk):
+    """``project_pair(*pool_blocks(query, key), ...)`` in one launch, for the
+    shapes of ``pool_project_applies``: returns ``qp [B,Hkv,nb,P]`` and
+    ``kp [B,Hkv,nb,2,P]`` float32, the same values (same operation order)
+    without the pooled summaries or a second launch."""
+    _cuda(query, "query")
+    _cuda(key, "key")
+    if not pool_project_applies(query, key, Wq, Wk):
+        raise ValueError("pool_project needs head_dim 128, [128, 128] float32 weights, bf16/fp16 inputs and "
+                         "at most 8 query heads per KV head")
+    B, Hq, T, D = query.shape
+    Hkv = key.shape[1]
+    P = Wq.shape[1]
+    nb = (T + BLOCK - 1) // BLOCK
+    Wq = Wq.to(query.device).contiguous()
+    Wk = Wk.to(query.device).contiguous()
+    qp = torch.empty((B, Hkv, nb, P), device=query.device, dtype=torch.float32)
+    kp = torch.empty((B, Hkv, nb, 2, P), device=query.device, dtype=torch.float32)
+    with torch.cuda.device(query.device):
+        rc = spruce_hip.lib().spruce_selector_pool_project(
+            spruce_hip.ptr(query), spruce_hip.strides(query), spruce_hip.ptr(key), spruce_hip.strides(key),
+            B, Hq, Hkv, T, D, spruce_hip.dtype_code(query), spruce_hip.ptr(Wq), spruce_hip.ptr(Wk), P,
+            spruce_hip.ptr(qp), spruce_hip.ptr(kp), spruce_hip.stream_of(query))
+    spruce_hip.check(rc, "spruce_selector_pool_project")
+    return qp, kp
+
+
 def project(x, W):
     """``x [..., D] @ W [D, P]`` in float32 with a sequential fused multiply-add over D."""
     _cuda(x, "x")
@@ -255,8 +306,15 @@ def select_blocks(query, key, Wq, Wk, top_k=32, return_intermediates=False):
 
     Returns ``selected`` int32 ``[B, 1, Hkv, nb, top_k]`` (the selected_blocks
     layout with one layer), or a dict with every intermediate when
-    ``return_intermediates``.
+    ``return_intermediates``.  Without intermediates, shapes that
+    ``pool_project_applies`` covers pool and project in one launch (same
+    values).
     """
+    if not return_intermediates and pool_project_applies(query, key, Wq, Wk):
+        qp, kp = pool_project(query, key, Wq, Wk)
+        B, Hkv, nb, P = qp.shape
+        sc = gate_scores(qp.reshape(B * Hkv, nb, 1, P), kp.reshape(B * Hkv, nb, 2, P), causal="lower")
+        return causal_topk_blocks(sc, top_k).reshape(B, Hkv, nb, top_k)[:, None]
     q_mean, k_sum = pool_blocks(query, key)
     B, Hkv, nb, D = q_mean.shape
     if Wq.shape == Wk.shape:

@@ -56,6 +56,8 @@ _SIGNATURES = {
     "spruce_gate_scores": [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, ctypes.c_int, _p, _p],
     "spruce_causal_topk": [_p, _i64, _i64, _i64, _i64, _p, _p],
     "spruce_select_flat_supported": [_i64, _i64, _i64, _i64, ctypes.c_int, _i64],
+    "spruce_selector_pool_project": [
+        _p, _STRIDES, _p, _STRIDES, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _p, _i64, _p, _p, _p],
     "spruce_select_flat": [
         _p, _STRIDES, _p, _STRIDES, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _p, _i64, ctypes.c_float,
         _i64, _p, _i64, _p, _p],

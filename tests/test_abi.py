@@ -227,3 +227,20 @@ def test_fused_selector_support_and_validation_before_launch():
     for kwargs, message in cases:
         assert call(**kwargs) == -1, kwargs
         assert message in spruce_hip.last_error(), (kwargs, spruce_hip.last_error())
+
+
+def test_pooled_projection_validation_before_launch():
+    lib = spruce_hip.lib()
+    fake = ctypes.c_void_p(1 << 20)
+    qs, ks = _strides(0, 128, 3584, 1), _strides(0, 128, 512, 1)
+
+    def call(Hq=28, D=128, dtype=0, P=128, qs=qs, out=fake, T=1000):
+        return lib.spruce_selector_pool_project(fake, qs, fake, ks, 1, Hq, 4, T, D, dtype, fake, fake, P, out,
+                                                fake, None)
+    cases = [(dict(D=64), "head_dim 128"), (dict(dtype=2), "16-bit"), (dict(Hq=36), "at most 8"),
+             (dict(P=64), "projection dim 128"), (dict(qs=_strides(0, 128, 100, 1)), "16-byte aligned"),
+             (dict(out=None), "non-null"), (dict(Hq=30), "invalid shape"),
+             (dict(qs=_strides(0, 128, 1 << 22, 1), T=1 << 10), "2^31")]
+    for kwargs, message in cases:
+        assert call(**kwargs) == -1, kwargs
+        assert message in spruce_hip.last_error(), (kwargs, spruce_hip.last_error())

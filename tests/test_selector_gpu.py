@@ -364,3 +364,42 @@ def test_fused_route_applies_only_to_its_shapes():
     assert not fused_route_applies(torch.zeros(1, 18, 256, 128, device=DEV, dtype=torch.bfloat16), k, W, W)  # G 9
     long_q = torch.zeros(1, 2, 1024 * 64 + 1, 128, device=DEV, dtype=torch.bfloat16)   # 1025 key blocks
     assert not fused_route_applies(long_q, long_q[:, :1], W, W)
+
+
+# Pooling + projection in one launch against the two launches it replaces,
+# bit for bit: every query heads per KV head from 1 to 8, ragged T, B > 1,
+# both 16-bit dtypes, [B, T, H, D] and [B, H, T, D] storage.
+@pytest.mark.parametrize("B,Hq,Hkv,T,dtype,bthd", [
+    (1, 28, 4, 4097, torch.bfloat16, True),
+    (2, 8, 2, 1000, torch.float16, False),
+    (1, 8, 1, 130, torch.bfloat16, True),
+    (3, 3, 3, 64, torch.float16, True),
+    (1, 10, 2, 70000, torch.bfloat16, False),   # more than 1024 blocks
+    (1, 12, 2, 77, torch.bfloat16, True),
+    (1, 4, 4, 3333, torch.float16, True),
+    (1, 6, 1, 640, torch.bfloat16, False),
+])
+def test_pool_project_equals_pool_then_project(B, Hq, Hkv, T, dtype, bthd):
+    from selector.select import pool_project, pool_project_applies
+    D = P = 128
+    print(f"pool_project B={B} Hq={Hq} Hkv={Hkv} T={T} {dtype}", flush=True)
+    gen = torch.Generator().manual_seed(T + Hq)
+    if bthd:
+        q = torch.randn(B, T, Hq, D, generator=gen).to(dtype).to(DEV).transpose(1, 2)
+        kk = torch.randn(B, T, Hkv, D, generator=gen).to(dtype).to(DEV).transpose(1, 2)
+    else:
+        q = torch.randn(B, Hq, T, D, generator=gen).to(dtype).to(DEV)
+        kk = torch.randn(B, Hkv, T, D, generator=gen).to(dtype).to(DEV)
+    Wq = (torch.randn(D, P, generator=gen) / D ** 0.5).to(DEV)
+    Wk = (torch.randn(D, P, generator=gen) / D ** 0.5).to(DEV)
+    assert pool_project_applies(q, kk, Wq, Wk)
+    qp, kp = pool_project(q, kk, Wq, Wk)
+    qm, ks = pool_blocks(q, kk)
+    eqp, ekp = project_pair(qm, Wq, ks, Wk)
+    torch.cuda.synchronize()
+    assert torch.equal(qp, eqp)
+    assert torch.equal(kp, ekp)
+    if T <= 1000:
+        exp = osel.flat_select(q.float().cpu().numpy(), kk.float().cpu().numpy(), Wq.cpu().numpy(),
+                               Wk.cpu().numpy(), top_k=8)
+        assert np.array_equal(_np(select_blocks(q, kk, Wq, Wk, top_k=8)), exp["selected"])
