@@ -310,13 +310,13 @@ def main():
             from selector.gate import FlatGate
             from selector.traversal import traverse_projected
             from selector.tree import build_key_tree
-            from teacher.chunked_extract import _proto_pool_seq, proto_pool_grouped
+            from teacher.chunked_extract import proto_pool_qk
             kb5, beam = T5 // 64, 16
             gate = FlatGate(1, D, proj_dim=D).to(dev).eval()
             div = math.sqrt(gate.proj_dim)
 
             def features():
-                return proto_pool_grouped(q5, Hkv, 64, 8), _proto_pool_seq(k5, 64, 8)
+                return proto_pool_qk(q5, k5, 64, 8)
 
             def project(qf, levels):
                 return gate.project_queries(qf), gate.project_key_levels([lvl.features for lvl in levels],
@@ -381,10 +381,10 @@ def main():
     # features (group-averaged Q, key prototypes; the Q prototypes pooled by
     # one small launch), against the same work done in separate passes.
     if not args.no_extra:
-        from teacher.chunked_extract import _proto_pool_seq, causal_prefill_features, proto_pool_grouped
+        from teacher.chunked_extract import causal_prefill_features, proto_pool_qk
         fnc = lambda: causal_prefill_features(q, k, v, scale, 8)  # noqa: E731
         fnu = lambda: (causal_prefill_features(q, k, v, scale, capture=False),  # noqa: E731
-                       proto_pool_grouped(q, Hkv, 64, 8), _proto_pool_seq(k, 64, 8))
+                       proto_pool_qk(q, k, 64, 8))
         _, kums = _time_launches(fnu, max(5, args.steps // 5), max(2, args.warmup // 5))
         _, kcms = _time_launches(fnc, max(5, args.steps // 5), max(2, args.warmup // 5))
         mc, mu = statistics.median(kcms), statistics.median(kums)
@@ -458,8 +458,8 @@ def main():
 
         # Selector prototype features of the reference's capture hook: Q
         # group-averaged and pooled to mean + 7 outliers per block, K likewise.
-        from teacher.chunked_extract import _proto_pool_seq, proto_pool_grouped
-        fnp = lambda: (proto_pool_grouped(q3, Hkv, 64, 8), _proto_pool_seq(k3, 64, 8))  # noqa: E731
+        from teacher.chunked_extract import proto_pool_qk
+        fnp = lambda: proto_pool_qk(q3, k3, 64, 8)  # noqa: E731
         _, kpms = _time_launches(fnp, max(10, args.steps // 2), max(3, args.warmup // 2))
         mp = statistics.median(kpms)
         byp = (Hq + Hkv) * T3 * D * 2 + 2 * Hkv * (T3 // 64) * 8 * D * 2

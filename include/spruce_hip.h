@@ -544,6 +544,18 @@ int spruce_proto_pool(const void* x, const int64_t xs[4], int64_t B, int64_t H, 
                       int64_t G, int64_t block, int64_t P, int dtype, void* out, void* stream);
 
 /*
+ * Query and key prototypes of the same blocks in one launch: out_q equals
+ * spruce_proto_pool(q, ..., H = Hq, G = Hkv, ...) and out_k equals
+ * spruce_proto_pool(k, ..., H = G = Hkv, ...) (teacher/chunked_extract.py:27-80
+ * on both sides, as the capture hook :145-147 calls them).  16-bit q and k
+ * with a contiguous last dim and 16-byte aligned rows, D a multiple of 8 up to
+ * 128, Hq / Hkv <= 8, 1 <= block <= 64, 1 <= P <= 65.
+ */
+int spruce_proto_pool_qk(const void* q, const int64_t qs[4], const void* k, const int64_t ks[4], int64_t B,
+                         int64_t Hq, int64_t Hkv, int64_t L, int64_t D, int64_t block, int64_t P, int dtype,
+                         void* out_q, void* out_k, void* stream);
+
+/*
  * Per-token group average, x [B, H, L, D] -> out [B, G, L, D] contiguous, x's
  * dtype.  Replaces _group_avg_tokens (teacher/chunked_extract.py:75-80).
  */

@@ -129,16 +129,39 @@ constexpr int kProtoBatch = 2;
 // one (91.5 vs 91.2 us).
 constexpr int kProtoAny = 0, kProtoGroup16 = 1, kProtoOne16 = 2;
 
-template <int PATH, bool F16>
-__global__ __launch_bounds__(256) void proto_pool_kernel(ProtoParams p) {
+// Rows of the block tile padded by 16 bytes: 16-byte aligned for the vector
+// distance reads and spread over the banks.
+template <bool T16>
+constexpr int proto_tstr() { return kProtoMaxD + (T16 ? 8 : 4); }
+constexpr int kProtoTileBytes = kProtoMaxBlock * (kProtoMaxD + 4) * 4;  // the float tile (the larger)
+
+// Raw 16-byte chunks of one head's block (the key side): kProtoBatchK per
+// thread cover a 64 x 128 block; chunks past the block load the last one
+// again (in range; not stored).
+__device__ __forceinline__ void load_block_raw(const ProtoParams& p, int b, int h0, int t0, int n,
+                                               uint4 (&raw)[kProtoBatchK]) {
+  const int dch = p.D >> 3;
+  const int ne = n * dch;
+  const uint16_t* xb = static_cast<const uint16_t*>(p.x) + (int64_t)b * p.xs[0] + (int64_t)h0 * p.xs[1];
+#pragma unroll
+  for (int k = 0; k < kProtoBatchK; ++k) {
+    const int e = min((int)threadIdx.x + 256 * k, ne - 1);
+    const int t = e / dch, c = e - (e / dch) * dch;
+    raw[k] = *reinterpret_cast<const uint4*>(xb + (int64_t)(t0 + t) * p.xs[2] + 8 * c);
+  }
+}
+
+// One (batch, KV group, block i) of proto_pool_kernel, with the block tile at
+// tile_mem (proto_tstr<T16>() elements per row).  With PRE (the one-head
+// 16-bit path, a block of at most 256 * kProtoBatchK chunks) the chunks in
+// kraw were loaded by load_block_raw and are stored instead of loaded.
+template <int PATH, bool F16, bool PRE>
+__device__ __forceinline__ void proto_pool_block(const ProtoParams& p, int b, int g, int i, void* tile_mem,
+                                                 float* mean, int* pick, const uint4 (&kraw)[kProtoBatchK]) {
   constexpr bool T16 = PATH == kProtoOne16;
   using TileT = std::conditional_t<T16, uint16_t, float>;
-  // Rows padded by 16 bytes: 16-byte aligned for the vector distance reads
-  // and spread over the banks.
-  constexpr int TSTR = kProtoMaxD + (T16 ? 8 : 4);
-  __shared__ __attribute__((aligned(16))) TileT tile[kProtoMaxBlock][TSTR];
-  __shared__ __attribute__((aligned(16))) float mean[kProtoMaxD];
-  __shared__ int pick[kProtoMaxP];
+  constexpr int TSTR = proto_tstr<T16>();
+  TileT (*tile)[TSTR] = reinterpret_cast<TileT (*)[TSTR]>(tile_mem);
   auto tget = [&](int t, int d) -> float {
     if constexpr (T16) {
       return unpack1<F16>(tile[t][d]);
@@ -147,10 +170,6 @@ __global__ __launch_bounds__(256) void proto_pool_kernel(ProtoParams p) {
     }
   };
   const int tid = threadIdx.x;
-  const int i = blockIdx.x % p.nb;
-  const int bg = blockIdx.x / p.nb;
-  const int g = bg % p.G;
-  const int b = bg / p.G;
   const int t0 = i * p.block;
   const int n = min(p.block, p.L - t0);
   const int h0 = g * p.rep;
@@ -211,7 +230,22 @@ __global__ __launch_bounds__(256) void proto_pool_kernel(ProtoParams p) {
     const int dch = p.D >> 3;
     const int ne = n * dch;  // 16-byte chunks of the block, >= 1
     const uint16_t* xb = static_cast<const uint16_t*>(p.x) + (int64_t)b * p.xs[0] + (int64_t)h0 * p.xs[1];
-    for (int e0 = tid; e0 < ne; e0 += 256 * kProtoBatchK) {
+    if constexpr (PRE) {
+      // Constant indices into kraw, so the chunks stay in registers.
+      static_assert(kProtoBatchK == 4, "four preloaded chunks per thread");
+      auto put = [&](int k, const uint4 v) __attribute__((always_inline)) {
+        const int e = tid + 256 * k;
+        if (e < ne) {
+          const int t = e / dch, c = e - (e / dch) * dch;
+          *reinterpret_cast<uint4*>(&tile[t][8 * c]) = v;
+        }
+      };
+      put(0, kraw[0]);
+      put(1, kraw[1]);
+      put(2, kraw[2]);
+      put(3, kraw[3]);
+    }
+    for (int e0 = tid; !PRE && e0 < ne; e0 += 256 * kProtoBatchK) {
       // Chunks past the block load the last one again (in range; not stored).
       uint4 raw[kProtoBatchK];
 #pragma unroll
@@ -319,6 +353,41 @@ __global__ __launch_bounds__(256) void proto_pool_kernel(ProtoParams p) {
   }
 }
 
+template <int PATH, bool F16>
+__global__ __launch_bounds__(256) void proto_pool_kernel(ProtoParams p) {
+  constexpr bool T16 = PATH == kProtoOne16;
+  __shared__ __attribute__((aligned(16))) char tile[kProtoMaxBlock * proto_tstr<T16>() * (T16 ? 2 : 4)];
+  __shared__ __attribute__((aligned(16))) float mean[kProtoMaxD];
+  __shared__ int pick[kProtoMaxP];
+  const int i = blockIdx.x % p.nb;
+  const int bg = blockIdx.x / p.nb;
+  const uint4 none[kProtoBatchK] = {};
+  proto_pool_block<PATH, F16, false>(p, bg / p.G, bg % p.G, i, tile, mean, pick, none);
+}
+
+// Query and key prototypes of the same (batch, KV group, block) in one
+// workgroup: the key block's raw loads are issued first and held in
+// registers while the query heads are averaged and pooled; then the key
+// block is pooled in the same LDS (its 16-bit tile over the dead float one).
+// Outputs equal proto_pool_kernel's on each side.
+template <int QPATH, bool F16>
+__global__ __launch_bounds__(256) void proto_pool_qk_kernel(ProtoParams pq, ProtoParams pk) {
+  __shared__ __attribute__((aligned(16))) char tile[kProtoTileBytes];
+  __shared__ __attribute__((aligned(16))) float mean[kProtoMaxD];
+  __shared__ int pick[kProtoMaxP];
+  const int i = blockIdx.x % pq.nb;
+  const int bg = blockIdx.x / pq.nb;
+  const int b = bg / pq.G, g = bg % pq.G;
+  const int t0 = i * pk.block;
+  const int n = min(pk.block, pk.L - t0);
+  uint4 kraw[kProtoBatchK];
+  load_block_raw(pk, b, g, t0, n, kraw);
+  const uint4 none[kProtoBatchK] = {};
+  proto_pool_block<QPATH, F16, false>(pq, b, g, i, tile, mean, pick, none);
+  __syncthreads();  // the query output has read the tile and the mean
+  proto_pool_block<kProtoOne16, F16, true>(pk, b, g, i, tile, mean, pick, kraw);
+}
+
 __global__ __launch_bounds__(256) void group_avg_kernel(ProtoParams p, int64_t total8) {
   // One thread per (b, g, t, 8-dim chunk) -- vector path only.
   const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -423,4 +492,36 @@ extern "C" int spruce_group_avg_tokens(const void* x, const int64_t xs[4], int64
                        (hipStream_t)stream, p, total);
   }
   return check_launch("group_avg_kernel");
+}
+
+extern "C" int spruce_proto_pool_qk(const void* q, const int64_t qs[4], const void* k, const int64_t ks[4],
+                                    int64_t B, int64_t Hq, int64_t Hkv, int64_t L, int64_t D, int64_t block,
+                                    int64_t P, int dtype, void* out_q, void* out_k, void* stream) {
+  ProtoParams pq, pk;
+  int rc = fill_params(pq, q, qs, B, Hq, L, D, Hkv, dtype, out_q);
+  if (rc) return rc;
+  rc = fill_params(pk, k, ks, B, Hkv, L, D, Hkv, dtype, out_k);
+  if (rc) return rc;
+  SPRUCE_REQUIRE(dtype != SPRUCE_DTYPE_F32 && D % 8 == 0 && D <= kProtoMaxD && qs[3] == 1 && ks[3] == 1 &&
+                     pq.rep <= 8,
+                 "fused query/key prototypes need 16-bit inputs with a contiguous last dim, head_dim a multiple "
+                 "of 8 up to %d and at most 8 query heads per KV head",
+                 kProtoMaxD);
+  SPRUCE_REQUIRE(block >= 1 && block <= kProtoMaxBlock, "block must be in [1, %d], got %lld", kProtoMaxBlock,
+                 (long long)block);
+  SPRUCE_REQUIRE(P >= 1 && P <= kProtoMaxP, "P must be in [1, %d], got %lld", kProtoMaxP, (long long)P);
+  pq.block = pk.block = (int)block;
+  pq.P = pk.P = (int)P;
+  pq.nb = pk.nb = (int)((L + block - 1) / block);
+  const int64_t grid = B * Hkv * (int64_t)pq.nb;
+  SPRUCE_REQUIRE(grid < ((int64_t)1 << 31), "too many blocks");
+  const bool f16 = dtype == SPRUCE_DTYPE_F16;
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, pq, pk);
+  };
+  if (pq.rep == 1)
+    f16 ? launch(proto_pool_qk_kernel<kProtoOne16, true>) : launch(proto_pool_qk_kernel<kProtoOne16, false>);
+  else
+    f16 ? launch(proto_pool_qk_kernel<kProtoGroup16, true>) : launch(proto_pool_qk_kernel<kProtoGroup16, false>);
+  return check_launch("proto_pool_qk_kernel");
 }

@@ -74,6 +74,8 @@ _SIGNATURES = {
     "spruce_pack_selected_ids": [_p, ctypes.c_int, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "spruce_pack_selected_mask": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "spruce_proto_pool": [_p, _STRIDES, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _p],
+    "spruce_proto_pool_qk": [_p, _STRIDES, _p, _STRIDES, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_int,
+                             _p, _p, _p],
     "spruce_kv_summary": [
         _p, _STRIDES, _p, _STRIDES, _i64, _i64, _i64, _i64, ctypes.c_int, _p, _p, _p, _i64,
         _p, _p, _p, _p, _p, ctypes.c_size_t, _p],

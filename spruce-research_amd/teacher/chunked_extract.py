@@ -124,6 +124,40 @@ def proto_pool_grouped(query, G, block=_BLOCK, P=_PROTO):
     return _launch_proto(query, G, block, P)
 
 
+def _aligned16(x):
+    return x.data_ptr() % 16 == 0 and all((s * x.element_size()) % 16 == 0 for s in x.stride()[:3])
+
+
+@torch.no_grad()
+def proto_pool_qk(query, key, block=_BLOCK, P=_PROTO):
+    """``(proto_pool_grouped(query, G, block, P), _proto_pool_seq(key, block, P))``
+    with G = key's head count, in one launch when both are 16-bit with
+    16-byte aligned rows, head_dim a multiple of 8 up to 128 and at most 8
+    query heads per KV head (each block's key loads then overlap its query
+    work); otherwise the two launches.  The same values either way."""
+    _features_input(query, "proto_pool_qk")
+    _features_input(key, "proto_pool_qk")
+    b, H, L, d = query.shape
+    G = key.shape[1]
+    if key.shape[0] != b or key.shape[2:] != query.shape[2:] or H % G:
+        raise ValueError(f"key {tuple(key.shape)} does not match query {tuple(query.shape)}")
+    fused = (query.dtype == key.dtype and query.dtype in (torch.bfloat16, torch.float16) and d % 8 == 0
+             and d <= 128 and H // G <= 8 and 1 <= block <= 64 and query.stride(-1) == 1 and key.stride(-1) == 1
+             and _aligned16(query) and _aligned16(key))
+    if not fused:
+        return proto_pool_grouped(query, G, block, P), _proto_pool_seq(key, block, P)
+    nb = (L + block - 1) // block
+    out_q = torch.empty((b, G, nb, P, d), device=query.device, dtype=query.dtype)
+    out_k = torch.empty((b, G, nb, P, d), device=query.device, dtype=query.dtype)
+    with torch.cuda.device(query.device):
+        rc = spruce_hip.lib().spruce_proto_pool_qk(
+            spruce_hip.ptr(query), spruce_hip.strides(query), spruce_hip.ptr(key), spruce_hip.strides(key),
+            b, H, G, L, d, block, P, spruce_hip.dtype_code(query), spruce_hip.ptr(out_q), spruce_hip.ptr(out_k),
+            spruce_hip.stream_of(query))
+    spruce_hip.check(rc, "spruce_proto_pool_qk")
+    return out_q, out_k
+
+
 @torch.no_grad()
 def _group_avg_tokens(x, G):
     """[b,H,L,d] -> [b,G,L,d]: the H/G query heads of each KV group averaged per token."""
@@ -231,10 +265,8 @@ def _propagate(query, key, value, scaling, dropout):
 
 
 def _capture_qk(module, query, key):
-    groups = key.shape[1]
-    pooled_q = proto_pool_grouped(query, groups, _BLOCK, _PROTO).cpu()
-    pooled_k = _proto_pool_seq(key, _BLOCK, _PROTO).cpu()
-    _CAPTURE_QK[module.layer_idx] = (pooled_q, pooled_k)
+    pooled_q, pooled_k = proto_pool_qk(query, key, _BLOCK, _PROTO)
+    _CAPTURE_QK[module.layer_idx] = (pooled_q.cpu(), pooled_k.cpu())
 
 
 def _capture_fused(module, query, key, value, scaling):

@@ -244,3 +244,18 @@ def test_pooled_projection_validation_before_launch():
     for kwargs, message in cases:
         assert call(**kwargs) == -1, kwargs
         assert message in spruce_hip.last_error(), (kwargs, spruce_hip.last_error())
+
+
+def test_proto_pool_qk_validation_before_launch():
+    lib = spruce_hip.lib()
+    fake = ctypes.c_void_p(1 << 20)
+    qs, ks = _strides(0, 128, 3584, 1), _strides(0, 128, 512, 1)
+
+    def call(Hq=28, D=128, dtype=0, block=64, P=8, qs=qs, out=fake):
+        return lib.spruce_proto_pool_qk(fake, qs, fake, ks, 1, Hq, 4, 1000, D, block, P, dtype, out, fake, None)
+    cases = [(dict(dtype=2), "16-bit"), (dict(D=12), "multiple of 8"), (dict(Hq=36), "at most 8"),
+             (dict(block=65), "block must be"), (dict(P=66), "P must be"), (dict(out=None), "non-null"),
+             (dict(qs=_strides(0, 128, 100, 1)), "16-byte aligned"), (dict(Hq=30), "not divisible")]
+    for kwargs, message in cases:
+        assert call(**kwargs) == -1, kwargs
+        assert message in spruce_hip.last_error(), (kwargs, spruce_hip.last_error())

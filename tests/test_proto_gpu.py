@@ -110,3 +110,32 @@ def test_full_size_cfg3_one_group_and_invariants():
     # Mean prototype of every group equals the block mean of the group-averaged tokens.
     qm = q.float().reshape(1, 4, 7, 1024, 64, 128).mean(dim=(2, 4)).to(DEV)
     torch.testing.assert_close(pq[:, :, :, 0].float(), qm, atol=2e-2, rtol=1e-2)
+
+
+# Query and key prototypes in one launch against the two launches, bit for
+# bit: query heads per KV head 1, 4, 7 and 8, ragged L, blocks of 64 and 32,
+# 8 and 3 prototypes, both 16-bit dtypes, [B, T, H, D] and [B, H, T, D]
+# storage, head_dim 128 and 64.
+@pytest.mark.parametrize("dtype,B,Hq,Hkv,L,d,block,P,bthd", [
+    (torch.bfloat16, 1, 28, 4, 4097, 128, 64, 8, True),
+    (torch.float16, 2, 8, 2, 1000, 128, 64, 8, False),
+    (torch.bfloat16, 1, 8, 1, 130, 64, 32, 3, True),
+    (torch.float16, 1, 4, 4, 777, 128, 64, 8, True),
+    (torch.bfloat16, 2, 16, 2, 65, 128, 64, 65, False),
+])
+def test_proto_pool_qk_equals_two_launches(dtype, B, Hq, Hkv, L, d, block, P, bthd):
+    from teacher.chunked_extract import _proto_pool_seq, proto_pool_grouped, proto_pool_qk
+    print(f"proto_pool_qk {dtype} B={B} Hq={Hq} Hkv={Hkv} L={L} d={d} block={block} P={P}", flush=True)
+    g = torch.Generator().manual_seed(L + Hq)
+    if bthd:
+        q = torch.randn(B, L, Hq, d, generator=g).to(dtype).to("cuda").transpose(1, 2)
+        k = torch.randn(B, L, Hkv, d, generator=g).to(dtype).to("cuda").transpose(1, 2)
+    else:
+        q = torch.randn(B, Hq, L, d, generator=g).to(dtype).to("cuda")
+        k = torch.randn(B, Hkv, L, d, generator=g).to(dtype).to("cuda")
+    k[0, 0, 3, :8] = -0.0   # negative zeros survive the key side
+    fq, fk = proto_pool_qk(q, k, block, P)
+    eq, ek = proto_pool_grouped(q, Hkv, block, P), _proto_pool_seq(k, block, P)
+    torch.cuda.synchronize()
+    assert torch.equal(fq.view(torch.int16), eq.view(torch.int16))
+    assert torch.equal(fk.view(torch.int16), ek.view(torch.int16))
